@@ -1,0 +1,194 @@
+/*
+ * moe_amd — C ABI of the MI355X (gfx950) MoE expert-layer kernels.
+ *
+ * Every entry point takes raw device pointers, sizes and a hipStream_t passed
+ * as `void*` (the caller's current stream), enqueues its kernels on that
+ * stream and returns an int status (MOE_OK or a negative MOE_ERR_*).  Nothing
+ * synchronises the device and nothing reads device data back to the host.
+ * The library allocates no device memory: scratch comes from the caller
+ * through `workspace` arguments sized by the *_workspace_size() queries.
+ * moe_amd_last_error() returns the text of the last failure on this thread.
+ *
+ * Shapes: T tokens, H hidden, E experts, K top-k, I intermediate (moe
+ * intermediate size), S = T*K routed rows.  Layouts are row-major:
+ *   hidden_states [T,H], gate_up_proj [E,2I,H] (rows 0..I-1 gate, I..2I-1 up),
+ *   down_proj [E,H,I], topk_index [T,K] int64, topk_weights [T,K].
+ * Routed rows are ordered by expert (stable: token-major inside an expert);
+ * offsets[e] is the first routed row of expert e, offsets[E] the number of
+ * rows that belong to real experts (ids outside [0,E) are "sentinels": they
+ * sort behind every expert and contribute zero, as expert-parallel sentinels
+ * do in transformers' grouped_mm backend).
+ *
+ * Reference interfaces (leonmodal/moe at its pinned transformers 5.x):
+ *   router      src/models/modeling_qwen3_moe.py:266-275 (Qwen3MoeTopKRouter)
+ *               src/models/router.py:103-155           (DeepSeekRouter)
+ *   experts     transformers/integrations/moe.py:377-478 (grouped_mm_experts_forward)
+ *               registered through ExpertsInterface (integrations/moe.py:481-506)
+ */
+#ifndef MOE_AMD_H
+#define MOE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  MOE_OK = 0,
+  MOE_ERR_ARG = -1,         /* bad shape or argument            */
+  MOE_ERR_DTYPE = -2,       /* unsupported dtype code           */
+  MOE_ERR_ALIGN = -3,       /* pointer not 16-byte aligned      */
+  MOE_ERR_WORKSPACE = -4,   /* workspace missing or too small   */
+  MOE_ERR_HIP = -5,         /* HIP runtime / launch error       */
+  MOE_ERR_UNSUPPORTED = -6  /* valid request this build lacks   */
+};
+
+enum { MOE_DTYPE_F32 = 0, MOE_DTYPE_BF16 = 1 };
+
+/* Row-tile heights for which moe_amd_permute() writes tile prefix sums. */
+enum { MOE_NUM_TILE_SIZES = 3 };
+
+int moe_amd_abi_version(void);
+const char* moe_amd_last_error(void);
+
+/* ---------------------------------------------------------------- router */
+
+/* Softmax router after the gating linear: probs = softmax(float(logits) +
+ * logit_offset) over E, top-K (value descending, lower expert id first on
+ * equal values), optional renormalisation by the top-K sum (no epsilon).
+ * Replaces Qwen3MoeTopKRouter.forward lines 269-274 of
+ * src/models/modeling_qwen3_moe.py.  logit_offset [E] may be NULL.
+ * tokens_per_expert [E] (fp32, may be NULL) is incremented by the selection
+ * counts.  Outputs: probs [T,E] fp32, topk_weights [T,K] fp32,
+ * topk_index [T,K] int64. */
+int moe_amd_router_softmax_topk(const void* logits, int logits_dtype, const float* logit_offset,
+                                int64_t T, int E, int K, int renormalize, float* probs,
+                                float* topk_weights, int64_t* topk_index,
+                                float* tokens_per_expert, void* stream);
+
+/* Backward of the above (autograd of softmax -> gather -> renorm).  d_probs
+ * (gradient arriving on the returned router_logits, [T,E] fp32) may be NULL.
+ * Writes d_logits [T,E] in d_logits_dtype (the logits' dtype). */
+int moe_amd_router_softmax_topk_backward(const float* probs, const int64_t* topk_index,
+                                         const float* d_topk_weights, const float* d_probs,
+                                         int64_t T, int E, int K, int renormalize,
+                                         void* d_logits, int d_logits_dtype, void* stream);
+
+/* DeepSeek-V3 router after the fp32 gating linear: scores = sigmoid(logits);
+ * selection = top-K of scores + expert_bias (flat, or group-limited when
+ * num_groups > 0: groups scored by the sum of their top K/group_topk,
+ * group_topk groups kept); weights = gathered unbiased scores, divided by
+ * (sum + 1e-20) when renormalize, times scaling_factor when > 0, stored in
+ * weights_dtype.  Replaces DeepSeekRouter.forward lines 111-152 of
+ * src/models/router.py (group_limited_topk: lines 22-70).
+ * tokens_per_expert (may be NULL) accumulates the bincount of line 145. */
+int moe_amd_router_sigmoid_topk(const float* logits, const float* expert_bias, int64_t T, int E,
+                                int K, int renormalize, float scaling_factor, int num_groups,
+                                int group_topk, float* scores, void* topk_weights,
+                                int weights_dtype, int64_t* topk_index,
+                                float* tokens_per_expert, void* stream);
+
+/* Backward of the DeepSeek router's sigmoid -> gather -> renorm -> scale.
+ * d_topk_weights is in weights_dtype; d_scores [T,E] fp32 may be NULL.
+ * Writes d_logits [T,E] fp32. */
+int moe_amd_router_sigmoid_topk_backward(const float* scores, const int64_t* topk_index,
+                                         const void* d_topk_weights, int weights_dtype,
+                                         const float* d_scores, int64_t T, int E, int K,
+                                         int renormalize, float scaling_factor,
+                                         float* d_logits, void* stream);
+
+/* ----------------------------------------------------------- permutation */
+
+/* Workspace bytes moe_amd_permute() needs for S routed rows, E experts. */
+size_t moe_amd_permute_workspace_size(int64_t S, int E);
+
+/* Counting sort of the flattened topk_index [S] by expert id.  Replaces the
+ * sort / histc / cumsum of transformers/integrations/moe.py:389-403 (the
+ * reference sort is unstable; this one is stable).  Outputs (int32):
+ *   counts [E]            rows per expert (histc)
+ *   offsets [E+1]         exclusive prefix of counts; offsets[E] = rows
+ *                         owned by real experts (cumsum(counts)[-1])
+ *   row_src [S]           sorted row r -> flat routed index t*K+k (perm)
+ *   slot [S]              flat routed index -> sorted row (inverse perm)
+ *   tile_starts [3*(E+1)] exclusive prefix of ceil(counts/BM) for the
+ *                         row-tile heights BM = 64, 128, 256 (GEMM plan). */
+int moe_amd_permute(const int64_t* topk_index, int64_t S, int E, void* workspace,
+                    size_t workspace_bytes, int32_t* counts, int32_t* offsets, int32_t* row_src,
+                    int32_t* slot, int32_t* tile_starts, void* stream);
+
+/* ------------------------------------------------------- grouped GEMMs */
+/* All GEMMs: bf16 operands (dtype = MOE_DTYPE_BF16), fp32 accumulation,
+ * bf16 results; H and I must be multiples of 64; pointers 16-byte aligned.
+ * The expert of each routed row is found from offsets / tile_starts on the
+ * device, so empty and skewed experts cost no host synchronisation. */
+
+/* gate_up = xs @ gate_up_proj[e]^T with xs[r] = hidden_states[row_src[r]/K],
+ * then act = silu(gate) * up.  transformers/integrations/moe.py:439-447.
+ * gate_up_out [S,2I] (may be NULL: inference), act_out [S,I]. */
+int moe_amd_gemm_gate_up_swiglu(const void* hidden_states, const int32_t* row_src, int top_k,
+                                const int32_t* offsets, const int32_t* tile_starts,
+                                const void* gate_up_proj, int64_t T, int64_t S, int E, int H,
+                                int I, int dtype, void* gate_up_out, void* act_out,
+                                void* stream);
+
+/* y = act @ down_proj[e]^T.  transformers/integrations/moe.py:449-459.
+ * y_out [S,H]. */
+int moe_amd_gemm_down(const void* act, const int32_t* offsets, const int32_t* tile_starts,
+                      const void* down_proj, int64_t S, int E, int H, int I, int dtype,
+                      void* y_out, void* stream);
+
+/* Backward of GEMM-2 w.r.t. its input fused with the SwiGLU backward:
+ * d_act = dy @ down_proj[e]; (d_gate, d_up) from gate_up; writes
+ * d_gate_up [S,2I].  Autograd of integrations/moe.py:447,457 (formula :226-242). */
+int moe_amd_gemm_down_backward_dx_dswiglu(const void* dy, const int32_t* offsets,
+                                          const int32_t* tile_starts, const void* down_proj,
+                                          const void* gate_up, int64_t S, int E, int H, int I,
+                                          int dtype, void* d_gate_up, void* stream);
+
+/* d_down_proj[e] = dy_e^T @ act_e  ([E,H,I]; zero for empty experts). */
+int moe_amd_gemm_down_backward_dw(const void* dy, const void* act, const int32_t* offsets,
+                                  int64_t S, int E, int H, int I, int dtype, void* d_down_proj,
+                                  void* stream);
+
+/* d_xs = d_gate_up @ gate_up_proj[e]  ([S,H]). */
+int moe_amd_gemm_gate_up_backward_dx(const void* d_gate_up, const int32_t* offsets,
+                                     const int32_t* tile_starts, const void* gate_up_proj,
+                                     int64_t S, int E, int H, int I, int dtype, void* d_xs,
+                                     void* stream);
+
+/* d_gate_up_proj[e] = d_gate_up_e^T @ xs_e, xs gathered from hidden_states
+ * through row_src  ([E,2I,H]; zero for empty experts). */
+int moe_amd_gemm_gate_up_backward_dw(const void* d_gate_up, const void* hidden_states,
+                                     const int32_t* row_src, int top_k, const int32_t* offsets,
+                                     int64_t T, int64_t S, int E, int H, int I, int dtype,
+                                     void* d_gate_up_proj, void* stream);
+
+/* ------------------------------------------------------------- combine */
+
+/* out[t] = sum_k w[t,k] * y[slot[t*K+k]], accumulated in fp32 in k order,
+ * rounded once to dtype; sentinel rows contribute zero.  With bf16 weights
+ * each product is rounded to bf16 first (bf16 * bf16 in the reference).
+ * transformers/integrations/moe.py:461-478. */
+int moe_amd_combine(const void* y, const int32_t* slot, const int32_t* offsets,
+                    const void* topk_weights, int weights_dtype, int64_t T, int K, int E, int H,
+                    int dtype, void* out, void* stream);
+
+/* Backward of the combine: d_y[slot[t,k]] = d_out[t] * w[t,k] (rounded to
+ * dtype) and d_w[t,k] = <d_out[t], y[slot[t,k]]> (weights_dtype). */
+int moe_amd_combine_backward(const void* d_out, const void* y, const int32_t* slot,
+                             const int32_t* offsets, const void* topk_weights,
+                             int weights_dtype, int64_t T, int K, int E, int H, int dtype,
+                             void* d_y, void* d_topk_weights, void* stream);
+
+/* Backward of the gather xs = hidden_states[row_src // K]:
+ * d_x[t] = sum_k d_xs[slot[t*K+k]] (fp32 accumulation, sentinels skipped). */
+int moe_amd_gather_backward(const void* d_xs, const int32_t* slot, const int32_t* offsets,
+                            int64_t T, int K, int E, int H, int dtype, void* d_x, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOE_AMD_H */

@@ -1,0 +1,233 @@
+// Weighted combine (unpermute + sum over K) and the two gather-shaped
+// backward kernels of the expert layer.  All three are HBM-bound row
+// gathers: one wave per token, each lane moving 16 bytes per step, so every
+// routed row is read as full contiguous 128-byte lines.
+// Reference: transformers/integrations/moe.py:461-478 (forward combine) and
+// :393-395 (the hidden_states[perm // K] gather whose backward is dX).
+#include "common.h"
+
+namespace moe {
+namespace {
+
+constexpr int kWaves = 4;
+
+template <typename T> struct Vec;
+template <> struct Vec<bf16> {
+  static constexpr int N = 8;  // elements per 16-byte lane access
+  __device__ static void load(const bf16* p, float (&v)[8]) {
+    u32x4 w = *(const u32x4*)p;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { v[2 * i] = bf_lo(w[i]); v[2 * i + 1] = bf_hi(w[i]); }
+  }
+  __device__ static void store(bf16* p, const float (&v)[8]) {
+    u32x4 w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = pack_bf2(v[2 * i], v[2 * i + 1]);
+    *(u32x4*)p = w;
+  }
+};
+template <> struct Vec<float> {
+  static constexpr int N = 4;
+  __device__ static void load(const float* p, float (&v)[4]) {
+    f32x4 w = *(const f32x4*)p;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = w[i];
+  }
+  __device__ static void store(float* p, const float (&v)[4]) {
+    f32x4 w = {v[0], v[1], v[2], v[3]};
+    *(f32x4*)p = w;
+  }
+};
+
+__device__ __forceinline__ float load_w(const void* w, int wdt, int64_t i) {
+  return wdt == MOE_DTYPE_BF16 ? bf2f(((const bf16*)w)[i]) : ((const float*)w)[i];
+}
+
+template <typename T>
+__global__ __launch_bounds__(64 * kWaves) void combine_kernel(
+    const T* __restrict__ y, const int* __restrict__ slot, const int* __restrict__ offsets,
+    const void* __restrict__ w, int wdt, int64_t ntok, int K, int E, int H, T* __restrict__ out) {
+  constexpr int N = Vec<T>::N;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int nvalid = offsets[E];
+  const int64_t nw = (int64_t)gridDim.x * kWaves;
+  for (int64_t t = (int64_t)blockIdx.x * kWaves + wid; t < ntok; t += nw) {
+    for (int h0 = lane * N; h0 < H; h0 += 64 * N) {
+      float acc[N];
+#pragma unroll
+      for (int i = 0; i < N; ++i) acc[i] = 0.f;
+      for (int k = 0; k < K; ++k) {
+        const int s = slot[t * K + k];
+        if (s >= nvalid) continue;  // sentinel: masked to zero in the reference
+        const float wk = load_w(w, wdt, t * K + k);
+        float v[N];
+        Vec<T>::load(y + (int64_t)s * H + h0, v);
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+          float prod = v[i] * wk;
+          if (wdt == MOE_DTYPE_BF16 && sizeof(T) == 2) prod = round_bf(prod);
+          acc[i] += prod;
+        }
+      }
+      Vec<T>::store(out + t * H + h0, acc);
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(64 * kWaves) void combine_bwd_kernel(
+    const T* __restrict__ dout, const T* __restrict__ y, const int* __restrict__ slot,
+    const int* __restrict__ offsets, const void* __restrict__ w, int wdt, int64_t ntok, int K,
+    int E, int H, T* __restrict__ dy, void* __restrict__ dw) {
+  constexpr int N = Vec<T>::N;
+  const bool round_prod = (wdt == MOE_DTYPE_BF16 && sizeof(T) == 2);
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int nvalid = offsets[E];
+  const int64_t nw = (int64_t)gridDim.x * kWaves;
+  for (int64_t t = (int64_t)blockIdx.x * kWaves + wid; t < ntok; t += nw) {
+    for (int k = 0; k < K; ++k) {
+      const int s = slot[t * K + k];
+      const bool valid = s < nvalid;
+      const float wk = load_w(w, wdt, t * K + k);
+      float dot = 0.f;
+      if (valid) {
+        for (int h0 = lane * N; h0 < H; h0 += 64 * N) {
+          float g[N], v[N], d[N];
+          Vec<T>::load(dout + t * H + h0, g);
+          Vec<T>::load(y + (int64_t)s * H + h0, v);
+#pragma unroll
+          for (int i = 0; i < N; ++i) {
+            d[i] = g[i] * wk;
+            float pr = g[i] * v[i];
+            dot += round_prod ? round_bf(pr) : pr;
+          }
+          Vec<T>::store(dy + (int64_t)s * H + h0, d);
+        }
+      }
+      dot = wave_sum(dot);
+      if (lane == 0) {
+        if (wdt == MOE_DTYPE_BF16)
+          ((bf16*)dw)[t * K + k] = f2bf(dot);
+        else
+          ((float*)dw)[t * K + k] = dot;
+      }
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(64 * kWaves) void gather_bwd_kernel(
+    const T* __restrict__ dxs, const int* __restrict__ slot, const int* __restrict__ offsets,
+    int64_t ntok, int K, int E, int H, T* __restrict__ dx) {
+  constexpr int N = Vec<T>::N;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int nvalid = offsets[E];
+  const int64_t nw = (int64_t)gridDim.x * kWaves;
+  for (int64_t t = (int64_t)blockIdx.x * kWaves + wid; t < ntok; t += nw) {
+    for (int h0 = lane * N; h0 < H; h0 += 64 * N) {
+      float acc[N];
+#pragma unroll
+      for (int i = 0; i < N; ++i) acc[i] = 0.f;
+      for (int k = 0; k < K; ++k) {
+        const int s = slot[t * K + k];
+        if (s >= nvalid) continue;
+        float v[N];
+        Vec<T>::load(dxs + (int64_t)s * H + h0, v);
+#pragma unroll
+        for (int i = 0; i < N; ++i) acc[i] += v[i];
+      }
+      Vec<T>::store(dx + t * H + h0, acc);
+    }
+  }
+}
+
+int grid_tokens(int64_t ntok) {
+  int64_t b = (ntok + kWaves - 1) / kWaves;
+  if (b > 8192) b = 8192;
+  return (int)(b < 1 ? 1 : b);
+}
+
+int check_rows(int64_t T, int K, int E, int H, int dtype, const char* who) {
+  MOE_REQUIRE(dtype == MOE_DTYPE_BF16 || dtype == MOE_DTYPE_F32, MOE_ERR_DTYPE, "%s: dtype %d",
+              who, dtype);
+  MOE_REQUIRE(T >= 0 && K >= 1 && E >= 1 && H >= 1, MOE_ERR_ARG, "%s: bad sizes", who);
+  const int n = dtype == MOE_DTYPE_BF16 ? 8 : 4;
+  MOE_REQUIRE(H % n == 0, MOE_ERR_ARG, "%s: H=%d must be a multiple of %d", who, H, n);
+  return MOE_OK;
+}
+
+bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+}  // namespace
+}  // namespace moe
+
+using namespace moe;
+
+extern "C" int moe_amd_combine(const void* y, const int32_t* slot, const int32_t* offsets,
+                               const void* topk_weights, int weights_dtype, int64_t T, int K,
+                               int E, int H, int dtype, void* out, void* stream) {
+  const char* who = "combine";
+  int rc = check_rows(T, K, E, H, dtype, who);
+  if (rc) return rc;
+  MOE_REQUIRE(weights_dtype == MOE_DTYPE_BF16 || weights_dtype == MOE_DTYPE_F32, MOE_ERR_DTYPE,
+              "%s: weights dtype %d", who, weights_dtype);
+  MOE_REQUIRE(offsets && out && (T == 0 || (y && slot && topk_weights)), MOE_ERR_ARG,
+              "%s: null pointer", who);
+  MOE_REQUIRE(al16(out) && (T == 0 || al16(y)), MOE_ERR_ALIGN, "%s: misaligned pointer", who);
+  if (T == 0) return MOE_OK;
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == MOE_DTYPE_BF16)
+    combine_kernel<bf16><<<grid_tokens(T), 64 * kWaves, 0, st>>>(
+        (const bf16*)y, slot, offsets, topk_weights, weights_dtype, T, K, E, H, (bf16*)out);
+  else
+    combine_kernel<float><<<grid_tokens(T), 64 * kWaves, 0, st>>>(
+        (const float*)y, slot, offsets, topk_weights, weights_dtype, T, K, E, H, (float*)out);
+  return check_launch(who);
+}
+
+extern "C" int moe_amd_combine_backward(const void* d_out, const void* y, const int32_t* slot,
+                                        const int32_t* offsets, const void* topk_weights,
+                                        int weights_dtype, int64_t T, int K, int E, int H,
+                                        int dtype, void* d_y, void* d_topk_weights,
+                                        void* stream) {
+  const char* who = "combine_backward";
+  int rc = check_rows(T, K, E, H, dtype, who);
+  if (rc) return rc;
+  MOE_REQUIRE(weights_dtype == MOE_DTYPE_BF16 || weights_dtype == MOE_DTYPE_F32, MOE_ERR_DTYPE,
+              "%s: weights dtype %d", who, weights_dtype);
+  MOE_REQUIRE(offsets && (T == 0 || (d_out && y && slot && topk_weights && d_y && d_topk_weights)),
+              MOE_ERR_ARG, "%s: null pointer", who);
+  MOE_REQUIRE(T == 0 || (al16(d_out) && al16(y) && al16(d_y)), MOE_ERR_ALIGN,
+              "%s: misaligned pointer", who);
+  if (T == 0) return MOE_OK;
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == MOE_DTYPE_BF16)
+    combine_bwd_kernel<bf16><<<grid_tokens(T), 64 * kWaves, 0, st>>>(
+        (const bf16*)d_out, (const bf16*)y, slot, offsets, topk_weights, weights_dtype, T, K, E,
+        H, (bf16*)d_y, d_topk_weights);
+  else
+    combine_bwd_kernel<float><<<grid_tokens(T), 64 * kWaves, 0, st>>>(
+        (const float*)d_out, (const float*)y, slot, offsets, topk_weights, weights_dtype, T, K,
+        E, H, (float*)d_y, d_topk_weights);
+  return check_launch(who);
+}
+
+extern "C" int moe_amd_gather_backward(const void* d_xs, const int32_t* slot,
+                                       const int32_t* offsets, int64_t T, int K, int E, int H,
+                                       int dtype, void* d_x, void* stream) {
+  const char* who = "gather_backward";
+  int rc = check_rows(T, K, E, H, dtype, who);
+  if (rc) return rc;
+  MOE_REQUIRE(offsets && d_x && (T == 0 || (d_xs && slot)), MOE_ERR_ARG, "%s: null pointer",
+              who);
+  MOE_REQUIRE(al16(d_x) && (T == 0 || al16(d_xs)), MOE_ERR_ALIGN, "%s: misaligned pointer", who);
+  if (T == 0) return MOE_OK;
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == MOE_DTYPE_BF16)
+    gather_bwd_kernel<bf16><<<grid_tokens(T), 64 * kWaves, 0, st>>>(
+        (const bf16*)d_xs, slot, offsets, T, K, E, H, (bf16*)d_x);
+  else
+    gather_bwd_kernel<float><<<grid_tokens(T), 64 * kWaves, 0, st>>>(
+        (const float*)d_xs, slot, offsets, T, K, E, H, (float*)d_x);
+  return check_launch(who);
+}

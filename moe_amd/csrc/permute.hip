@@ -1,0 +1,216 @@
+// Token permutation: a stable counting sort of the S = T*K routed entries by
+// expert id, the GPU form of transformers' sort + histc + cumsum
+// (transformers/integrations/moe.py:389-403).
+//
+//   P1 histogram : one wave per 256-entry chunk, LDS atomics -> per-chunk
+//                  counts, stored expert-major [E+1][nchunks].
+//   P2 scan      : per-expert exclusive scan over chunks (one block per
+//                  expert) + one block that scans the expert totals into
+//                  offsets and the per-tile-height GEMM tile prefixes.
+//   P3 scatter   : each wave replays its chunk 64 entries at a time; a
+//                  ballot loop groups lanes by expert, the in-wave rank is
+//                  the popcount of lower peers, and a per-wave LDS counter
+//                  carries the rank across rounds -> stable order.
+// Ids outside [0,E) land in bin E (sentinels), after every real expert.
+#include "common.h"
+
+namespace moe {
+namespace {
+
+constexpr int kChunk = 256;        // entries per wave in P1/P3
+constexpr int kWaves = 4;          // waves per block in P1/P3
+constexpr int kTileSizes[MOE_NUM_TILE_SIZES] = {64, 128, 256};
+
+__device__ __forceinline__ int bin_of(int64_t id, int E) {
+  return (id >= 0 && id < E) ? (int)id : E;
+}
+
+__global__ __launch_bounds__(64 * kWaves) void hist_kernel(const int64_t* __restrict__ ids,
+                                                           int64_t S, int E, int64_t nch,
+                                                           int* __restrict__ chunk_hist) {
+  extern __shared__ int lds[];  // [kWaves][E+1]
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int64_t c = (int64_t)blockIdx.x * kWaves + wid;
+  int* h = lds + wid * (E + 1);
+  for (int e = lane; e <= E; e += 64) h[e] = 0;
+  __builtin_amdgcn_wave_barrier();
+  if (c < nch) {
+    const int64_t beg = c * kChunk;
+#pragma unroll
+    for (int i = 0; i < kChunk / 64; ++i) {
+      int64_t s = beg + i * 64 + lane;
+      if (s < S) atomicAdd(&h[bin_of(ids[s], E)], 1);
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  __syncthreads();
+  if (c < nch)
+    for (int e = lane; e <= E; e += 64) chunk_hist[(int64_t)e * nch + c] = h[e];
+}
+
+// Inclusive scan across one wave.
+__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    int u = __shfl_up(v, o, 64);
+    if (lane >= o) v += u;
+  }
+  return v;
+}
+
+// Exclusive scan across the block (blockDim.x multiple of 64, <= 1024).
+// Returns the exclusive prefix; *total receives the block sum.
+__device__ int block_excl_scan(int v, int* tmp /* >= 16 ints */, int* total) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  int inc = wave_incl_scan(v, lane);
+  if (lane == 63) tmp[wid] = inc;
+  __syncthreads();
+  if (wid == 0) {
+    int w = lane < nw ? tmp[lane] : 0;
+    int wi = wave_incl_scan(w, lane);
+    if (lane < nw) tmp[lane] = wi - w;
+    if (lane == nw - 1) tmp[16] = wi;
+  }
+  __syncthreads();
+  int res = inc - v + tmp[wid];
+  *total = tmp[16];
+  __syncthreads();
+  return res;
+}
+
+// One block per bin e: exclusive scan of chunk_hist[e][0..nch) in place.
+__global__ __launch_bounds__(256) void chunk_scan_kernel(int* __restrict__ chunk_hist,
+                                                         int64_t nch, int* __restrict__ totals) {
+  __shared__ int tmp[17];
+  const int e = blockIdx.x;
+  int* col = chunk_hist + (int64_t)e * nch;
+  int carry = 0;
+  for (int64_t base = 0; base < nch; base += blockDim.x) {
+    int64_t i = base + threadIdx.x;
+    int v = i < nch ? col[i] : 0;
+    int tot;
+    int ex = block_excl_scan(v, tmp, &tot);
+    if (i < nch) col[i] = carry + ex;
+    carry += tot;
+  }
+  if (threadIdx.x == 0) totals[e] = carry;
+}
+
+// Single block: offsets, counts and the GEMM tile prefixes.
+__global__ __launch_bounds__(1024) void finalize_kernel(const int* __restrict__ totals,
+                                                        int have_totals, int E,
+                                                        int* __restrict__ counts,
+                                                        int* __restrict__ offsets,
+                                                        int* __restrict__ tile_starts) {
+  __shared__ int tmp[17];
+  int carry[1 + MOE_NUM_TILE_SIZES] = {0, 0, 0, 0};
+  for (int base = 0; base <= E; base += blockDim.x) {
+    int e = base + threadIdx.x;
+    int n = (have_totals && e <= E) ? totals[e] : 0;
+    int tot;
+    int ex = block_excl_scan(n, tmp, &tot);
+    if (e <= E) {
+      offsets[e] = carry[0] + ex;
+      if (e < E) counts[e] = n;
+    }
+    carry[0] += tot;
+#pragma unroll
+    for (int b = 0; b < MOE_NUM_TILE_SIZES; ++b) {
+      int bm = kTileSizes[b];
+      int nt = (e < E) ? (n + bm - 1) / bm : 0;
+      int ext = block_excl_scan(nt, tmp, &tot);
+      if (e <= E) tile_starts[b * (E + 1) + e] = carry[1 + b] + ext;
+      carry[1 + b] += tot;
+    }
+  }
+}
+
+__global__ __launch_bounds__(64 * kWaves) void scatter_kernel(
+    const int64_t* __restrict__ ids, int64_t S, int E, int64_t nch,
+    const int* __restrict__ chunk_off, const int* __restrict__ offsets,
+    int* __restrict__ row_src, int* __restrict__ slot) {
+  extern __shared__ int lds[];  // [kWaves][E+1] running per-expert counters
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int64_t c = (int64_t)blockIdx.x * kWaves + wid;
+  int* cnt = lds + wid * (E + 1);
+  for (int e = lane; e <= E; e += 64) cnt[e] = 0;
+  __builtin_amdgcn_wave_barrier();
+  if (c >= nch) return;
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  const int64_t beg = c * kChunk;
+  for (int i = 0; i < kChunk / 64; ++i) {
+    const int64_t s = beg + i * 64 + lane;
+    const bool valid = s < S;
+    const int key = valid ? bin_of(ids[s], E) : -1;
+    // Group lanes by key: each pass peels off all lanes sharing the key of
+    // the lowest unassigned lane.
+    uint64_t todo = __ballot(valid);
+    uint64_t peers = 0;
+    while (todo) {
+      int leader = __builtin_ctzll(todo);
+      int lkey = __shfl(key, leader, 64);
+      uint64_t m = __ballot(key == lkey) & todo;
+      if (key == lkey) peers = m;
+      todo &= ~m;
+    }
+    int before = 0;
+    if (valid) before = cnt[key];
+    __builtin_amdgcn_wave_barrier();
+    if (valid) {
+      int rank = __popcll(peers & lt_mask);
+      int dest = offsets[key] + chunk_off[(int64_t)key * nch + c] + before + rank;
+      row_src[dest] = (int)s;
+      slot[s] = dest;
+      // Highest peer bumps the counter once for the whole group.
+      if ((peers >> lane) == 1ull) cnt[key] = before + __popcll(peers);
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
+size_t permute_ws_bytes(int64_t S, int E) {
+  int64_t nch = (S + kChunk - 1) / kChunk;
+  return align_up(((size_t)(E + 1) * (size_t)nch + (size_t)(E + 1)) * sizeof(int), 256);
+}
+
+}  // namespace
+}  // namespace moe
+
+using namespace moe;
+
+extern "C" size_t moe_amd_permute_workspace_size(int64_t S, int E) {
+  if (S < 0 || E < 1) return 0;
+  return permute_ws_bytes(S, E);
+}
+
+extern "C" int moe_amd_permute(const int64_t* topk_index, int64_t S, int E, void* workspace,
+                               size_t workspace_bytes, int32_t* counts, int32_t* offsets,
+                               int32_t* row_src, int32_t* slot, int32_t* tile_starts,
+                               void* stream) {
+  MOE_REQUIRE(S >= 0 && S < (int64_t)1 << 31, MOE_ERR_ARG, "permute: S=%lld out of range",
+              (long long)S);
+  MOE_REQUIRE(E >= 1 && E <= 16384, MOE_ERR_ARG, "permute: E=%d out of range", E);
+  MOE_REQUIRE(counts && offsets && tile_starts, MOE_ERR_ARG, "permute: null output");
+  MOE_REQUIRE(S == 0 || (topk_index && row_src && slot), MOE_ERR_ARG, "permute: null pointer");
+  const size_t need = permute_ws_bytes(S, E);
+  MOE_REQUIRE(workspace && workspace_bytes >= need, MOE_ERR_WORKSPACE,
+              "permute: workspace %zu bytes < %zu needed", workspace_bytes, need);
+  const size_t lds = (size_t)kWaves * (E + 1) * sizeof(int);
+  MOE_REQUIRE(lds <= 160 * 1024, MOE_ERR_ARG, "permute: E=%d needs too much LDS", E);
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t nch = (S + kChunk - 1) / kChunk;
+  int* chunk_hist = (int*)workspace;
+  int* totals = chunk_hist + (size_t)(E + 1) * nch;
+  if (nch > 0) {
+    const int blocks = (int)((nch + kWaves - 1) / kWaves);
+    hist_kernel<<<blocks, 64 * kWaves, lds, st>>>(topk_index, S, E, nch, chunk_hist);
+    chunk_scan_kernel<<<E + 1, 256, 0, st>>>(chunk_hist, nch, totals);
+  }
+  finalize_kernel<<<1, 1024, 0, st>>>(totals, nch > 0 ? 1 : 0, E, counts, offsets, tile_starts);
+  if (nch > 0) {
+    const int blocks = (int)((nch + kWaves - 1) / kWaves);
+    scatter_kernel<<<blocks, 64 * kWaves, lds, st>>>(topk_index, S, E, nch, chunk_hist,
+                                                     offsets, row_src, slot);
+  }
+  return check_launch("permute");
+}

@@ -1,0 +1,461 @@
+// Router kernels: softmax top-k (Qwen3MoeTopKRouter) and sigmoid + expert
+// bias top-k (DeepSeekRouter), forward and backward.
+//
+// One wave64 owns one token at a time.  The token's E scores live in
+// registers, NV = ceil(E/64) per lane (expert e = j*64 + lane), and the
+// top-K is extracted with K rounds of a wave-wide arg-max over
+// (value, -expert id), so equal values resolve to the lower expert id.
+// Reference: src/models/modeling_qwen3_moe.py:266-275,
+//            src/models/router.py:22-70 and :103-155.
+#include "common.h"
+
+#include <cmath>
+
+namespace moe {
+namespace {
+
+constexpr int kWavesPerBlock = 4;
+constexpr int kMaxExperts = 4096;  // NV <= 64
+
+__device__ __forceinline__ float load_logit(const void* p, int dtype, int64_t i) {
+  return dtype == MOE_DTYPE_BF16 ? bf2f(((const bf16*)p)[i]) : ((const float*)p)[i];
+}
+
+// True when candidate (va, ea) ranks before (vb, eb).
+__device__ __forceinline__ bool ranks_before(float va, int ea, float vb, int eb) {
+  return va > vb || (va == vb && ea < eb);
+}
+
+// Wave-wide arg-max of (v, e) under ranks_before; every lane gets the result.
+__device__ __forceinline__ void wave_argmax(float& v, int& e) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    float ov = __shfl_xor(v, o, 64);
+    int oe = __shfl_xor(e, o, 64);
+    if (ranks_before(ov, oe, v, e)) { v = ov; e = oe; }
+  }
+}
+
+// Best not-yet-taken entry held by this lane (e = j*64 + lane).
+template <int NV>
+__device__ __forceinline__ void lane_best(const float (&val)[NV], uint64_t taken, int lane,
+                                          float& bv, int& be) {
+  bv = -INFINITY;
+  be = 0x7fffffff;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    if (!((taken >> j) & 1ull)) {
+      int e = j * 64 + lane;
+      if (ranks_before(val[j], e, bv, be)) { bv = val[j]; be = e; }
+    }
+  }
+}
+
+// Extracts the K best of val (not in `taken`) in rank order; lane k < K
+// receives the k-th selected expert id (other lanes get 0).
+template <int NV>
+__device__ __forceinline__ int wave_topk(const float (&val)[NV], uint64_t taken, int lane, int K) {
+  int mine = 0;
+  for (int k = 0; k < K; ++k) {
+    float bv;
+    int be;
+    lane_best<NV>(val, taken, lane, bv, be);
+    wave_argmax(bv, be);
+    if (lane == k) mine = be;
+    if ((be & 63) == lane) taken |= 1ull << (be >> 6);
+  }
+  return mine;
+}
+
+template <int NV>
+__global__ __launch_bounds__(64 * kWavesPerBlock) void softmax_topk_kernel(
+    const void* __restrict__ logits, int logits_dtype, const float* __restrict__ offset,
+    int64_t T, int E, int K, int renorm, float* __restrict__ probs, float* __restrict__ topk_w,
+    int64_t* __restrict__ topk_idx, float* __restrict__ tpe) {
+  extern __shared__ int hist[];  // [E] when tpe != nullptr
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  if (tpe) {
+    for (int e = threadIdx.x; e < E; e += blockDim.x) hist[e] = 0;
+    __syncthreads();
+  }
+  const int64_t nwaves = (int64_t)gridDim.x * kWavesPerBlock;
+  for (int64_t t = (int64_t)blockIdx.x * kWavesPerBlock + wid; t < T; t += nwaves) {
+    float v[NV];
+    uint64_t taken = 0;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      int e = j * 64 + lane;
+      if (e < E) {
+        v[j] = load_logit(logits, logits_dtype, t * E + e) + (offset ? offset[e] : 0.0f);
+      } else {
+        v[j] = -INFINITY;
+        taken |= 1ull << j;
+      }
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) m = fmaxf(m, v[j]);
+    m = wave_max(m);
+    float p[NV];
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      p[j] = (j * 64 + lane < E) ? expf(v[j] - m) : 0.f;
+      s += p[j];
+    }
+    s = wave_sum(s);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      p[j] = p[j] / s;
+      int e = j * 64 + lane;
+      if (e < E) probs[t * E + e] = p[j];
+    }
+    // Softmax is monotone, so ranking the (offset) logits ranks the probs;
+    // equal logits give bit-equal probs and resolve to the lower expert id.
+    const int ek = wave_topk<NV>(v, taken, lane, K);
+    // Lane k fetches the prob of its selected expert from the owner lane.
+    float wk = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      float pj = __shfl(p[j], ek & 63, 64);
+      if ((ek >> 6) == j) wk = pj;
+    }
+    if (renorm) {
+      // Sum in rank order on every lane (K <= 64 values broadcast one by one).
+      float ssum = 0.f;
+      for (int k = 0; k < K; ++k) ssum += __shfl(wk, k, 64);
+      wk = wk / ssum;
+    }
+    if (lane < K) {
+      topk_w[t * K + lane] = wk;
+      topk_idx[t * K + lane] = ek;
+      if (tpe && ek >= 0 && ek < E) atomicAdd(&hist[ek], 1);
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+  if (tpe) {
+    __syncthreads();
+    for (int e = threadIdx.x; e < E; e += blockDim.x)
+      if (hist[e]) atomicAdd(&tpe[e], (float)hist[e]);
+  }
+}
+
+template <int NV>
+__global__ __launch_bounds__(64 * kWavesPerBlock) void sigmoid_topk_kernel(
+    const float* __restrict__ logits, const float* __restrict__ bias, int64_t T, int E, int K,
+    int renorm, float scaling, int num_groups, int group_topk, float* __restrict__ scores,
+    void* __restrict__ topk_w, int w_dtype, int64_t* __restrict__ topk_idx,
+    float* __restrict__ tpe) {
+  extern __shared__ int hist[];
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  if (tpe) {
+    for (int e = threadIdx.x; e < E; e += blockDim.x) hist[e] = 0;
+    __syncthreads();
+  }
+  const int64_t nwaves = (int64_t)gridDim.x * kWavesPerBlock;
+  for (int64_t t = (int64_t)blockIdx.x * kWavesPerBlock + wid; t < T; t += nwaves) {
+    float s[NV], b[NV];
+    uint64_t taken = 0;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      int e = j * 64 + lane;
+      if (e < E) {
+        s[j] = sigmoidf_(logits[t * E + e]);
+        scores[t * E + e] = s[j];
+        b[j] = s[j] + (bias ? bias[e] : 0.0f);
+      } else {
+        s[j] = 0.f;
+        b[j] = -INFINITY;
+        taken |= 1ull << j;
+      }
+    }
+    if (num_groups > 0) {
+      // Group-limited selection (router.py:22-70): score each group by the
+      // sum of its top (K / group_topk) biased scores, keep group_topk groups.
+      const int eg = E / num_groups, per = K / group_topk;
+      float gv = -INFINITY;  // lane g holds group g's score
+      for (int g = 0; g < num_groups; ++g) {
+        uint64_t gtaken = taken;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+          int e = j * 64 + lane;
+          if (e / eg != g) gtaken |= 1ull << j;
+        }
+        float acc = 0.f;
+        for (int q = 0; q < per; ++q) {
+          float bv;
+          int be;
+          lane_best<NV>(b, gtaken, lane, bv, be);
+          wave_argmax(bv, be);
+          acc += bv;
+          if ((be & 63) == lane) gtaken |= 1ull << (be >> 6);
+        }
+        if (lane == g) gv = acc;
+      }
+      // Pick group_topk groups (higher score first, lower group id on ties).
+      int gi = lane < num_groups ? lane : 0x7fffffff;
+      uint64_t keep = 0;
+      bool gone = lane >= num_groups;
+      for (int q = 0; q < group_topk; ++q) {
+        float bv = gone ? -INFINITY : gv;
+        int be = gone ? 0x7fffffff : gi;
+        wave_argmax(bv, be);
+        keep |= 1ull << be;
+        if (be == lane) gone = true;
+      }
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        int e = j * 64 + lane;
+        if (e < E && !((keep >> (e / eg)) & 1ull)) taken |= 1ull << j;
+      }
+    }
+    const int ek = wave_topk<NV>(b, taken, lane, K);
+    float wk = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      float sj = __shfl(s[j], ek & 63, 64);
+      if ((ek >> 6) == j) wk = sj;
+    }
+    if (renorm) {
+      float ssum = 0.f;
+      for (int k = 0; k < K; ++k) ssum += __shfl(wk, k, 64);
+      wk = wk / (ssum + 1e-20f);
+    }
+    if (scaling > 0.f) wk = wk * scaling;
+    if (lane < K) {
+      if (w_dtype == MOE_DTYPE_BF16)
+        ((bf16*)topk_w)[t * K + lane] = f2bf(wk);
+      else
+        ((float*)topk_w)[t * K + lane] = wk;
+      topk_idx[t * K + lane] = ek;
+      if (tpe && ek >= 0 && ek < E) atomicAdd(&hist[ek], 1);
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+  if (tpe) {
+    __syncthreads();
+    for (int e = threadIdx.x; e < E; e += blockDim.x)
+      if (hist[e]) atomicAdd(&tpe[e], (float)hist[e]);
+  }
+}
+
+// d(renormalised weights) -> d(gathered values): w_k = v_k / (S + eps).
+// Every lane k < K holds (v_k, g_k); returns dv_k.
+__device__ __forceinline__ float renorm_backward(float vk, float gk, int K, float eps) {
+  float ssum = 0.f, gv = 0.f;
+  for (int k = 0; k < K; ++k) {
+    ssum += __shfl(vk, k, 64);
+    gv += __shfl(gk * vk, k, 64);
+  }
+  float den = ssum + eps;
+  return gk / den - gv / (den * den);
+}
+
+template <int NV>
+__global__ __launch_bounds__(64 * kWavesPerBlock) void softmax_topk_bwd_kernel(
+    const float* __restrict__ probs, const int64_t* __restrict__ idx,
+    const float* __restrict__ dw, const float* __restrict__ dprobs, int64_t T, int E, int K,
+    int renorm, void* __restrict__ dlogits, int dl_dtype) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int64_t nwaves = (int64_t)gridDim.x * kWavesPerBlock;
+  for (int64_t t = (int64_t)blockIdx.x * kWavesPerBlock + wid; t < T; t += nwaves) {
+    int ek = lane < K ? (int)idx[t * K + lane] : -1;
+    float vk = lane < K ? probs[t * E + ek] : 0.f;
+    float gk = lane < K ? dw[t * K + lane] : 0.f;
+    float dv = renorm ? renorm_backward(vk, gk, K, 0.f) : gk;
+    float p[NV], dp[NV];
+    float dot = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      int e = j * 64 + lane;
+      p[j] = e < E ? probs[t * E + e] : 0.f;
+      dp[j] = (e < E && dprobs) ? dprobs[t * E + e] : 0.f;
+    }
+    for (int k = 0; k < K; ++k) {
+      int e = __shfl(ek, k, 64);
+      float g = __shfl(dv, k, 64);
+#pragma unroll
+      for (int j = 0; j < NV; ++j)
+        if (e == j * 64 + lane) dp[j] += g;
+    }
+#pragma unroll
+    for (int j = 0; j < NV; ++j) dot += p[j] * dp[j];
+    dot = wave_sum(dot);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      int e = j * 64 + lane;
+      if (e < E) {
+        float g = (dp[j] - dot) * p[j];
+        if (dl_dtype == MOE_DTYPE_BF16)
+          ((bf16*)dlogits)[t * E + e] = f2bf(g);
+        else
+          ((float*)dlogits)[t * E + e] = g;
+      }
+    }
+  }
+}
+
+template <int NV>
+__global__ __launch_bounds__(64 * kWavesPerBlock) void sigmoid_topk_bwd_kernel(
+    const float* __restrict__ scores, const int64_t* __restrict__ idx,
+    const void* __restrict__ dw, int w_dtype, const float* __restrict__ dscores, int64_t T,
+    int E, int K, int renorm, float scaling, float* __restrict__ dlogits) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int64_t nwaves = (int64_t)gridDim.x * kWavesPerBlock;
+  for (int64_t t = (int64_t)blockIdx.x * kWavesPerBlock + wid; t < T; t += nwaves) {
+    int ek = lane < K ? (int)idx[t * K + lane] : -1;
+    float vk = lane < K ? scores[t * E + ek] : 0.f;
+    float gk = 0.f;
+    if (lane < K)
+      gk = w_dtype == MOE_DTYPE_BF16 ? bf2f(((const bf16*)dw)[t * K + lane])
+                                     : ((const float*)dw)[t * K + lane];
+    if (scaling > 0.f) gk *= scaling;
+    float dv = renorm ? renorm_backward(vk, gk, K, 1e-20f) : gk;
+    float ds[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      int e = j * 64 + lane;
+      ds[j] = (e < E && dscores) ? dscores[t * E + e] : 0.f;
+    }
+    for (int k = 0; k < K; ++k) {
+      int e = __shfl(ek, k, 64);
+      float g = __shfl(dv, k, 64);
+#pragma unroll
+      for (int j = 0; j < NV; ++j)
+        if (e == j * 64 + lane) ds[j] += g;
+    }
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      int e = j * 64 + lane;
+      if (e < E) {
+        float y = scores[t * E + e];
+        dlogits[t * E + e] = ds[j] * (1.f - y) * y;
+      }
+    }
+  }
+}
+
+int grid_for(int64_t T) {
+  int64_t waves = T;
+  int64_t blocks = (waves + kWavesPerBlock - 1) / kWavesPerBlock;
+  if (blocks > 4096) blocks = 4096;
+  if (blocks < 1) blocks = 1;
+  return (int)blocks;
+}
+
+#define MOE_DISPATCH_NV(E, KERNEL, ...)                          \
+  do {                                                           \
+    int nv_ = ((E) + 63) / 64;                                   \
+    if (nv_ <= 1) KERNEL<1><<<__VA_ARGS__;                       \
+    else if (nv_ <= 2) KERNEL<2><<<__VA_ARGS__;                  \
+    else if (nv_ <= 4) KERNEL<4><<<__VA_ARGS__;                  \
+    else if (nv_ <= 8) KERNEL<8><<<__VA_ARGS__;                  \
+    else if (nv_ <= 16) KERNEL<16><<<__VA_ARGS__;                \
+    else if (nv_ <= 32) KERNEL<32><<<__VA_ARGS__;                \
+    else KERNEL<64><<<__VA_ARGS__;                               \
+  } while (0)
+
+int check_router_shape(int64_t T, int E, int K) {
+  MOE_REQUIRE(T >= 0, MOE_ERR_ARG, "router: T=%lld must be >= 0", (long long)T);
+  MOE_REQUIRE(E >= 1 && E <= kMaxExperts, MOE_ERR_ARG, "router: E=%d outside [1,%d]", E,
+              kMaxExperts);
+  MOE_REQUIRE(K >= 1 && K <= E && K <= 64, MOE_ERR_ARG, "router: K=%d outside [1,min(E,64)]",
+              K);
+  return MOE_OK;
+}
+
+}  // namespace
+}  // namespace moe
+
+using namespace moe;
+
+extern "C" int moe_amd_router_softmax_topk(const void* logits, int logits_dtype,
+                                           const float* logit_offset, int64_t T, int E, int K,
+                                           int renormalize, float* probs, float* topk_weights,
+                                           int64_t* topk_index, float* tokens_per_expert,
+                                           void* stream) {
+  int rc = check_router_shape(T, E, K);
+  if (rc) return rc;
+  MOE_REQUIRE(logits_dtype == MOE_DTYPE_F32 || logits_dtype == MOE_DTYPE_BF16, MOE_ERR_DTYPE,
+              "router_softmax_topk: logits dtype %d", logits_dtype);
+  MOE_REQUIRE(logits && probs && topk_weights && topk_index, MOE_ERR_ARG,
+              "router_softmax_topk: null pointer");
+  if (T == 0) return MOE_OK;
+  size_t shm = tokens_per_expert ? (size_t)E * sizeof(int) : 0;
+  MOE_DISPATCH_NV(E, softmax_topk_kernel, grid_for(T), 64 * kWavesPerBlock, shm,
+                  (hipStream_t)stream >>>(logits, logits_dtype, logit_offset, T, E, K,
+                                          renormalize, probs, topk_weights, topk_index,
+                                          tokens_per_expert));
+  return check_launch("router_softmax_topk");
+}
+
+extern "C" int moe_amd_router_softmax_topk_backward(const float* probs, const int64_t* topk_index,
+                                                    const float* d_topk_weights,
+                                                    const float* d_probs, int64_t T, int E,
+                                                    int K, int renormalize, void* d_logits,
+                                                    int d_logits_dtype, void* stream) {
+  int rc = check_router_shape(T, E, K);
+  if (rc) return rc;
+  MOE_REQUIRE(d_logits_dtype == MOE_DTYPE_F32 || d_logits_dtype == MOE_DTYPE_BF16,
+              MOE_ERR_DTYPE, "router_softmax_topk_backward: dtype %d", d_logits_dtype);
+  MOE_REQUIRE(probs && topk_index && d_topk_weights && d_logits, MOE_ERR_ARG,
+              "router_softmax_topk_backward: null pointer");
+  if (T == 0) return MOE_OK;
+  MOE_DISPATCH_NV(E, softmax_topk_bwd_kernel, grid_for(T), 64 * kWavesPerBlock, 0,
+                  (hipStream_t)stream >>>(probs, topk_index, d_topk_weights, d_probs, T, E, K,
+                                          renormalize, d_logits, d_logits_dtype));
+  return check_launch("router_softmax_topk_backward");
+}
+
+extern "C" int moe_amd_router_sigmoid_topk(const float* logits, const float* expert_bias,
+                                           int64_t T, int E, int K, int renormalize,
+                                           float scaling_factor, int num_groups, int group_topk,
+                                           float* scores, void* topk_weights, int weights_dtype,
+                                           int64_t* topk_index, float* tokens_per_expert,
+                                           void* stream) {
+  int rc = check_router_shape(T, E, K);
+  if (rc) return rc;
+  MOE_REQUIRE(weights_dtype == MOE_DTYPE_F32 || weights_dtype == MOE_DTYPE_BF16, MOE_ERR_DTYPE,
+              "router_sigmoid_topk: weights dtype %d", weights_dtype);
+  MOE_REQUIRE(logits && scores && topk_weights && topk_index, MOE_ERR_ARG,
+              "router_sigmoid_topk: null pointer");
+  if (num_groups > 0) {
+    MOE_REQUIRE(num_groups <= 64 && E % num_groups == 0 && group_topk >= 1 &&
+                    group_topk <= num_groups && K % group_topk == 0 &&
+                    (E / num_groups) * group_topk >= K,
+                MOE_ERR_ARG,
+                "router_sigmoid_topk: bad grouping (E=%d K=%d groups=%d group_topk=%d)", E, K,
+                num_groups, group_topk);
+  }
+  if (T == 0) return MOE_OK;
+  if (!(scaling_factor > 0.f)) scaling_factor = 0.f;
+  size_t shm = tokens_per_expert ? (size_t)E * sizeof(int) : 0;
+  MOE_DISPATCH_NV(E, sigmoid_topk_kernel, grid_for(T), 64 * kWavesPerBlock, shm,
+                  (hipStream_t)stream >>>(logits, expert_bias, T, E, K, renormalize,
+                                          scaling_factor, num_groups, group_topk, scores,
+                                          topk_weights, weights_dtype, topk_index,
+                                          tokens_per_expert));
+  return check_launch("router_sigmoid_topk");
+}
+
+extern "C" int moe_amd_router_sigmoid_topk_backward(const float* scores,
+                                                    const int64_t* topk_index,
+                                                    const void* d_topk_weights,
+                                                    int weights_dtype, const float* d_scores,
+                                                    int64_t T, int E, int K, int renormalize,
+                                                    float scaling_factor, float* d_logits,
+                                                    void* stream) {
+  int rc = check_router_shape(T, E, K);
+  if (rc) return rc;
+  MOE_REQUIRE(weights_dtype == MOE_DTYPE_F32 || weights_dtype == MOE_DTYPE_BF16, MOE_ERR_DTYPE,
+              "router_sigmoid_topk_backward: weights dtype %d", weights_dtype);
+  MOE_REQUIRE(scores && topk_index && d_topk_weights && d_logits, MOE_ERR_ARG,
+              "router_sigmoid_topk_backward: null pointer");
+  if (T == 0) return MOE_OK;
+  if (!(scaling_factor > 0.f)) scaling_factor = 0.f;
+  MOE_DISPATCH_NV(E, sigmoid_topk_bwd_kernel, grid_for(T), 64 * kWavesPerBlock, 0,
+                  (hipStream_t)stream >>>(scores, topk_index, d_topk_weights, weights_dtype,
+                                          d_scores, T, E, K, renormalize, scaling_factor,
+                                          d_logits));
+  return check_launch("router_sigmoid_topk_backward");
+}

@@ -1,0 +1,78 @@
+"""Whole MoE layer (gate + experts) as one function and one module.
+
+``moe_layer`` is the GPU form of Qwen3MoeSparseMoeBlock.forward
+(src/models/modeling_qwen3_moe.py:284-289) with either router: flatten to
+[T,H], gating linear (torch), HIP router kernel, HIP expert layer.
+``SparseMoeBlock`` wraps it with the reference's parameter names
+(``gate.weight``, ``experts.gate_up_proj``, ``experts.down_proj``).
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from .experts import experts_forward
+from .router import SigmoidTopKFunction, SoftmaxTopKFunction
+
+
+def moe_layer(x: torch.Tensor, w_router: torch.Tensor, gate_up_proj: torch.Tensor,
+              down_proj: torch.Tensor, top_k: int, router: str = "softmax",
+              renormalize: bool = True, logit_offset: torch.Tensor | None = None,
+              expert_bias: torch.Tensor | None = None, scaling_factor: float | None = None,
+              num_groups: int | None = None, group_topk: int | None = None,
+              tokens_per_expert: torch.Tensor | None = None):
+    """Returns (out [T,H], router_logits [T,E] fp32, weights [T,K], index [T,K])."""
+    if router == "softmax":
+        logits = F.linear(x, w_router)
+        probs, w, idx = SoftmaxTopKFunction.apply(logits, top_k, renormalize, logit_offset)
+    elif router == "sigmoid":
+        logits = F.linear(x.float(), w_router.float())
+        probs, w, idx = SigmoidTopKFunction.apply(logits, expert_bias, top_k, renormalize,
+                                                  scaling_factor, num_groups, group_topk,
+                                                  x.dtype, tokens_per_expert)
+    else:
+        raise ValueError(f"unknown router {router!r}")
+    out = experts_forward(x, idx, w, gate_up_proj, down_proj)
+    return out, probs, w, idx
+
+
+class _Gate(nn.Module):
+    def __init__(self, E: int, H: int):
+        super().__init__()
+        self.weight = nn.Parameter(torch.zeros(E, H))
+
+
+class _Bank(nn.Module):
+    def __init__(self, E: int, H: int, I: int):
+        super().__init__()
+        self.gate_up_proj = nn.Parameter(torch.empty(E, 2 * I, H))
+        self.down_proj = nn.Parameter(torch.empty(E, H, I))
+
+
+class SparseMoeBlock(nn.Module):
+    """Stand-alone MoE block: [B,S,H] (or [T,H]) -> same shape.  The last
+    router outputs are kept in ``router_logits`` / ``topk_index``."""
+
+    def __init__(self, hidden_size: int, num_experts: int, top_k: int, intermediate_size: int,
+                 router: str = "softmax", norm_topk_prob: bool = True):
+        super().__init__()
+        self.top_k = top_k
+        self.router = router
+        self.norm_topk_prob = norm_topk_prob
+        self.gate = _Gate(num_experts, hidden_size)
+        self.experts = _Bank(num_experts, hidden_size, intermediate_size)
+        self.logit_offset: torch.Tensor | None = None
+        self.register_buffer("expert_bias", torch.zeros(num_experts, dtype=torch.float32))
+        self.router_logits = None
+        self.topk_index = None
+
+    def forward(self, hidden_states: torch.Tensor) -> torch.Tensor:
+        shape = hidden_states.shape
+        flat = hidden_states.reshape(-1, shape[-1])
+        out, probs, _, idx = moe_layer(
+            flat, self.gate.weight, self.experts.gate_up_proj, self.experts.down_proj, self.top_k,
+            router=self.router, renormalize=self.norm_topk_prob, logit_offset=self.logit_offset,
+            expert_bias=self.expert_bias if self.router == "sigmoid" else None)
+        self.router_logits, self.topk_index = probs, idx
+        return out.reshape(shape)

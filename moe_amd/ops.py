@@ -1,0 +1,309 @@
+"""Tensor-level wrappers of the HIP kernels (one function per C entry point).
+
+Every function takes device tensors, allocates its outputs (and workspace)
+through torch's caching allocator, enqueues the kernel on torch's current
+stream and returns.  Nothing synchronises and nothing falls back to a CPU
+path: non-CUDA tensors or a missing library raise.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+
+TILE_SIZES = (64, 128, 256)
+
+# Optional per-launch timing: when a list is installed with
+# record_kernel_times(), every entry point brackets its launch with a pair of
+# HIP events on the current stream (the stream the kernels run on).
+_events: list | None = None
+
+
+def record_kernel_times(events: list | None) -> None:
+    """Install (a list) or remove (None) the per-launch event recorder.
+    Entries are (entry_point_name, start_event, end_event)."""
+    global _events
+    _events = events
+
+
+def _call(name: str, *args) -> None:
+    if _events is None:
+        _lib.call(name, *args)
+        return
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    _lib.call(name, *args)
+    end.record()
+    _events.append((name, start, end))
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.bfloat16:
+        return _lib.DTYPE_BF16
+    if dt == torch.float32:
+        return _lib.DTYPE_F32
+    raise TypeError(f"moe_amd: unsupported dtype {dt}")
+
+
+def _need_cuda(*ts: torch.Tensor | None) -> None:
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError(
+                "moe_amd kernels run on the GPU only; got a tensor on "
+                f"{t.device} (there is no CPU fallback)")
+
+
+def _contig(t: torch.Tensor) -> torch.Tensor:
+    return t if t.is_contiguous() else t.contiguous()
+
+
+# ----------------------------------------------------------------- router
+
+def router_softmax_topk(logits: torch.Tensor, top_k: int, renormalize: bool = True,
+                        logit_offset: torch.Tensor | None = None,
+                        tokens_per_expert: torch.Tensor | None = None):
+    """softmax(logits (+offset)) -> top-k -> renorm.  Returns (probs fp32 [T,E],
+    weights fp32 [T,K], index int64 [T,K])."""
+    _need_cuda(logits, logit_offset, tokens_per_expert)
+    logits = _contig(logits)
+    T, E = logits.shape
+    dev = logits.device
+    probs = torch.empty(T, E, device=dev, dtype=torch.float32)
+    w = torch.empty(T, top_k, device=dev, dtype=torch.float32)
+    idx = torch.empty(T, top_k, device=dev, dtype=torch.int64)
+    if logit_offset is not None:
+        logit_offset = _contig(logit_offset.to(torch.float32))
+    if tokens_per_expert is not None:
+        assert tokens_per_expert.dtype == torch.float32 and tokens_per_expert.is_contiguous()
+    _call("moe_amd_router_softmax_topk", logits.data_ptr(), _dtype_code(logits.dtype),
+          _ptr(logit_offset), T, E, top_k, int(renormalize), probs.data_ptr(),
+          w.data_ptr(), idx.data_ptr(), _ptr(tokens_per_expert), _stream(logits))
+    return probs, w, idx
+
+
+def router_softmax_topk_backward(probs, topk_index, d_weights, d_probs, renormalize: bool,
+                                 logits_dtype: torch.dtype):
+    _need_cuda(probs, topk_index, d_weights, d_probs)
+    T, E = probs.shape
+    K = topk_index.shape[1]
+    d_weights = _contig(d_weights.to(torch.float32))
+    if d_probs is not None:
+        d_probs = _contig(d_probs.to(torch.float32))
+    d_logits = torch.empty(T, E, device=probs.device, dtype=logits_dtype)
+    _call("moe_amd_router_softmax_topk_backward", probs.data_ptr(), topk_index.data_ptr(),
+          d_weights.data_ptr(), _ptr(d_probs), T, E, K, int(renormalize),
+          d_logits.data_ptr(), _dtype_code(logits_dtype), _stream(probs))
+    return d_logits
+
+
+def router_sigmoid_topk(logits: torch.Tensor, expert_bias: torch.Tensor | None, top_k: int,
+                        renormalize: bool = True, scaling_factor: float | None = None,
+                        num_groups: int | None = None, group_topk: int | None = None,
+                        weights_dtype: torch.dtype = torch.float32,
+                        tokens_per_expert: torch.Tensor | None = None):
+    """DeepSeek-V3 routing on fp32 logits.  Returns (scores fp32 [T,E],
+    weights [T,K] in weights_dtype, index int64 [T,K])."""
+    _need_cuda(logits, expert_bias, tokens_per_expert)
+    if logits.dtype != torch.float32:
+        raise TypeError("router_sigmoid_topk expects fp32 logits (the gating linear runs in fp32)")
+    logits = _contig(logits)
+    T, E = logits.shape
+    dev = logits.device
+    scores = torch.empty(T, E, device=dev, dtype=torch.float32)
+    w = torch.empty(T, top_k, device=dev, dtype=weights_dtype)
+    idx = torch.empty(T, top_k, device=dev, dtype=torch.int64)
+    if expert_bias is not None:
+        expert_bias = _contig(expert_bias.to(torch.float32))
+    grouped = num_groups is not None and group_topk is not None
+    _call("moe_amd_router_sigmoid_topk", logits.data_ptr(), _ptr(expert_bias), T, E, top_k,
+          int(renormalize), float(scaling_factor or 0.0), int(num_groups) if grouped else 0,
+          int(group_topk) if grouped else 0, scores.data_ptr(), w.data_ptr(),
+          _dtype_code(weights_dtype), idx.data_ptr(), _ptr(tokens_per_expert),
+          _stream(logits))
+    return scores, w, idx
+
+
+def router_sigmoid_topk_backward(scores, topk_index, d_weights, d_scores, renormalize: bool,
+                                 scaling_factor: float | None):
+    _need_cuda(scores, topk_index, d_weights, d_scores)
+    T, E = scores.shape
+    K = topk_index.shape[1]
+    d_weights = _contig(d_weights)
+    if d_scores is not None:
+        d_scores = _contig(d_scores.to(torch.float32))
+    d_logits = torch.empty(T, E, device=scores.device, dtype=torch.float32)
+    _call("moe_amd_router_sigmoid_topk_backward", scores.data_ptr(), topk_index.data_ptr(),
+          d_weights.data_ptr(), _dtype_code(d_weights.dtype), _ptr(d_scores), T, E, K,
+          int(renormalize), float(scaling_factor or 0.0), d_logits.data_ptr(),
+          _stream(scores))
+    return d_logits
+
+
+# ------------------------------------------------------------ permutation
+
+@dataclass
+class RoutingPlan:
+    """Device-side routing metadata produced by :func:`permute`.
+
+    counts [E], offsets [E+1] (exclusive; offsets[E] = rows of real experts),
+    row_src [S] (sorted row -> flat t*K+k), slot [S] (flat -> sorted row),
+    tile_starts [3, E+1] (row-tile prefixes for BM = 64/128/256)."""
+    counts: torch.Tensor
+    offsets: torch.Tensor
+    row_src: torch.Tensor
+    slot: torch.Tensor
+    tile_starts: torch.Tensor
+    num_experts: int
+    top_k: int
+    num_tokens: int
+
+    @property
+    def num_rows(self) -> int:
+        return self.row_src.numel()
+
+
+def permute(topk_index: torch.Tensor, num_experts: int) -> RoutingPlan:
+    """Stable counting sort of the routed (token, k) entries by expert."""
+    _need_cuda(topk_index)
+    if topk_index.dtype != torch.int64:
+        topk_index = topk_index.to(torch.int64)
+    topk_index = _contig(topk_index)
+    T, K = topk_index.shape
+    S = T * K
+    E = int(num_experts)
+    dev = topk_index.device
+    lib = _lib.load()
+    ws_bytes = int(lib.moe_amd_permute_workspace_size(S, E))
+    ws = torch.empty(max(ws_bytes, 256), device=dev, dtype=torch.uint8)
+    counts = torch.empty(E, device=dev, dtype=torch.int32)
+    offsets = torch.empty(E + 1, device=dev, dtype=torch.int32)
+    row_src = torch.empty(S, device=dev, dtype=torch.int32)
+    slot = torch.empty(S, device=dev, dtype=torch.int32)
+    tile_starts = torch.empty(_lib.NUM_TILE_SIZES, E + 1, device=dev, dtype=torch.int32)
+    _call("moe_amd_permute", topk_index.data_ptr(), S, E, ws.data_ptr(), ws.numel(),
+          counts.data_ptr(), offsets.data_ptr(), row_src.data_ptr(), slot.data_ptr(),
+          tile_starts.data_ptr(), _stream(topk_index))
+    return RoutingPlan(counts, offsets, row_src, slot, tile_starts, E, K, T)
+
+
+# --------------------------------------------------------- grouped GEMMs
+
+def gemm_gate_up_swiglu(x: torch.Tensor, plan: RoutingPlan, gate_up_proj: torch.Tensor,
+                        save_gate_up: bool = True):
+    """Returns (gate_up [S,2I] or None, act [S,I])."""
+    _need_cuda(x, gate_up_proj)
+    E, I2, H = gate_up_proj.shape
+    I = I2 // 2
+    S = plan.num_rows
+    act = torch.empty(S, I, device=x.device, dtype=x.dtype)
+    gu = torch.empty(S, I2, device=x.device, dtype=x.dtype) if save_gate_up else None
+    _call("moe_amd_gemm_gate_up_swiglu", x.data_ptr(), plan.row_src.data_ptr(), plan.top_k,
+          plan.offsets.data_ptr(), plan.tile_starts.data_ptr(), gate_up_proj.data_ptr(),
+          plan.num_tokens, S, E, H, I, _dtype_code(x.dtype), _ptr(gu), act.data_ptr(),
+          _stream(x))
+    return gu, act
+
+
+def gemm_down(act: torch.Tensor, plan: RoutingPlan, down_proj: torch.Tensor) -> torch.Tensor:
+    _need_cuda(act, down_proj)
+    E, H, I = down_proj.shape
+    S = plan.num_rows
+    y = torch.empty(S, H, device=act.device, dtype=act.dtype)
+    _call("moe_amd_gemm_down", act.data_ptr(), plan.offsets.data_ptr(),
+          plan.tile_starts.data_ptr(), down_proj.data_ptr(), S, E, H, I,
+          _dtype_code(act.dtype), y.data_ptr(), _stream(act))
+    return y
+
+
+def gemm_down_backward_dx_dswiglu(dy, plan: RoutingPlan, down_proj, gate_up):
+    _need_cuda(dy, down_proj, gate_up)
+    E, H, I = down_proj.shape
+    S = plan.num_rows
+    dgu = torch.empty(S, 2 * I, device=dy.device, dtype=dy.dtype)
+    _call("moe_amd_gemm_down_backward_dx_dswiglu", dy.data_ptr(), plan.offsets.data_ptr(),
+          plan.tile_starts.data_ptr(), down_proj.data_ptr(), gate_up.data_ptr(), S, E, H, I,
+          _dtype_code(dy.dtype), dgu.data_ptr(), _stream(dy))
+    return dgu
+
+
+def gemm_down_backward_dw(dy, act, plan: RoutingPlan, down_proj_shape, out=None):
+    _need_cuda(dy, act)
+    E, H, I = down_proj_shape
+    S = plan.num_rows
+    dw = out if out is not None else torch.empty(E, H, I, device=dy.device, dtype=dy.dtype)
+    _call("moe_amd_gemm_down_backward_dw", dy.data_ptr(), act.data_ptr(),
+          plan.offsets.data_ptr(), S, E, H, I, _dtype_code(dy.dtype), dw.data_ptr(),
+          _stream(dy))
+    return dw
+
+
+def gemm_gate_up_backward_dx(dgu, plan: RoutingPlan, gate_up_proj):
+    _need_cuda(dgu, gate_up_proj)
+    E, I2, H = gate_up_proj.shape
+    S = plan.num_rows
+    dxs = torch.empty(S, H, device=dgu.device, dtype=dgu.dtype)
+    _call("moe_amd_gemm_gate_up_backward_dx", dgu.data_ptr(), plan.offsets.data_ptr(),
+          plan.tile_starts.data_ptr(), gate_up_proj.data_ptr(), S, E, H, I2 // 2,
+          _dtype_code(dgu.dtype), dxs.data_ptr(), _stream(dgu))
+    return dxs
+
+
+def gemm_gate_up_backward_dw(dgu, x, plan: RoutingPlan, gate_up_proj_shape, out=None):
+    _need_cuda(dgu, x)
+    E, I2, H = gate_up_proj_shape
+    S = plan.num_rows
+    dw = out if out is not None else torch.empty(E, I2, H, device=dgu.device, dtype=dgu.dtype)
+    _call("moe_amd_gemm_gate_up_backward_dw", dgu.data_ptr(), x.data_ptr(),
+          plan.row_src.data_ptr(), plan.top_k, plan.offsets.data_ptr(), plan.num_tokens, S,
+          E, H, I2 // 2, _dtype_code(dgu.dtype), dw.data_ptr(), _stream(dgu))
+    return dw
+
+
+# ---------------------------------------------------------------- combine
+
+def combine(y: torch.Tensor, plan: RoutingPlan, topk_weights: torch.Tensor) -> torch.Tensor:
+    _need_cuda(y, topk_weights)
+    topk_weights = _contig(topk_weights)
+    T, K, E = plan.num_tokens, plan.top_k, plan.num_experts
+    H = y.shape[1]
+    out = torch.empty(T, H, device=y.device, dtype=y.dtype)
+    _call("moe_amd_combine", y.data_ptr(), plan.slot.data_ptr(), plan.offsets.data_ptr(),
+          topk_weights.data_ptr(), _dtype_code(topk_weights.dtype), T, K, E, H,
+          _dtype_code(y.dtype), out.data_ptr(), _stream(y))
+    return out
+
+
+def combine_backward(d_out, y, plan: RoutingPlan, topk_weights):
+    _need_cuda(d_out, y, topk_weights)
+    d_out = _contig(d_out)
+    topk_weights = _contig(topk_weights)
+    T, K, E = plan.num_tokens, plan.top_k, plan.num_experts
+    H = y.shape[1]
+    dy = torch.empty_like(y)
+    dw = torch.empty(T, K, device=y.device, dtype=topk_weights.dtype)
+    _call("moe_amd_combine_backward", d_out.data_ptr(), y.data_ptr(), plan.slot.data_ptr(),
+          plan.offsets.data_ptr(), topk_weights.data_ptr(), _dtype_code(topk_weights.dtype),
+          T, K, E, H, _dtype_code(y.dtype), dy.data_ptr(), dw.data_ptr(), _stream(y))
+    return dy, dw
+
+
+def gather_backward(dxs, plan: RoutingPlan) -> torch.Tensor:
+    _need_cuda(dxs)
+    T, K, E = plan.num_tokens, plan.top_k, plan.num_experts
+    H = dxs.shape[1]
+    dx = torch.empty(T, H, device=dxs.device, dtype=dxs.dtype)
+    _call("moe_amd_gather_backward", dxs.data_ptr(), plan.slot.data_ptr(),
+          plan.offsets.data_ptr(), T, K, E, H, _dtype_code(dxs.dtype), dx.data_ptr(),
+          _stream(dxs))
+    return dx

@@ -1,0 +1,150 @@
+"""Router modules whose softmax / sigmoid + top-k run in the HIP router kernel.
+
+Both subclass transformers' ``Qwen3MoeTopKRouter`` so that HF's
+OutputRecorder keeps capturing index 0 of their output as router_logits
+(src/models/modeling_qwen3_moe.py:375-379; the reason the reference's
+DeepSeekRouter subclasses it, src/models/router.py:73-79).  The gating linear
+stays a torch ``F.linear`` so its logits are bit-identical to the reference's
+on the same device.
+"""
+from __future__ import annotations
+
+from types import SimpleNamespace
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from . import ops
+
+try:  # the plug-in base class of the reference's routers
+    from transformers.models.qwen3_moe.modeling_qwen3_moe import Qwen3MoeTopKRouter as _RouterBase
+except Exception:  # pragma: no cover - transformers absent: plain module base
+    class _RouterBase(nn.Module):  # type: ignore[no-redef]
+        def __init__(self, config):
+            super().__init__()
+            self.top_k = config.num_experts_per_tok
+            self.num_experts = config.num_experts
+            self.norm_topk_prob = config.norm_topk_prob
+            self.hidden_dim = config.hidden_size
+            self.weight = nn.Parameter(torch.zeros(self.num_experts, self.hidden_dim))
+
+
+class SoftmaxTopKFunction(torch.autograd.Function):
+    """(logits) -> (probs, weights, index) with the softmax router's backward."""
+
+    @staticmethod
+    def forward(ctx, logits, top_k, renormalize, logit_offset):
+        probs, w, idx = ops.router_softmax_topk(logits, top_k, renormalize, logit_offset)
+        ctx.save_for_backward(probs, idx)
+        ctx.renormalize = renormalize
+        ctx.logits_dtype = logits.dtype
+        ctx.mark_non_differentiable(idx)
+        return probs, w, idx
+
+    @staticmethod
+    def backward(ctx, d_probs, d_w, d_idx):
+        probs, idx = ctx.saved_tensors
+        if d_w is None:
+            d_w = torch.zeros(idx.shape, device=idx.device, dtype=torch.float32)
+        d_logits = ops.router_softmax_topk_backward(probs, idx, d_w, d_probs, ctx.renormalize,
+                                                    ctx.logits_dtype)
+        return d_logits, None, None, None
+
+
+class SigmoidTopKFunction(torch.autograd.Function):
+    """(fp32 logits) -> (scores, weights, index) for the DeepSeek-V3 router."""
+
+    @staticmethod
+    def forward(ctx, logits, expert_bias, top_k, renormalize, scaling_factor, num_groups,
+                group_topk, weights_dtype, tokens_per_expert):
+        scores, w, idx = ops.router_sigmoid_topk(
+            logits, expert_bias, top_k, renormalize, scaling_factor, num_groups, group_topk,
+            weights_dtype, tokens_per_expert)
+        ctx.save_for_backward(scores, idx)
+        ctx.renormalize = renormalize
+        ctx.scaling_factor = scaling_factor
+        ctx.w_dtype = weights_dtype
+        ctx.mark_non_differentiable(idx)
+        return scores, w, idx
+
+    @staticmethod
+    def backward(ctx, d_scores, d_w, d_idx):
+        scores, idx = ctx.saved_tensors
+        if d_w is None:
+            d_w = torch.zeros(idx.shape, device=idx.device, dtype=ctx.w_dtype)
+        d_logits = ops.router_sigmoid_topk_backward(scores, idx, d_w.to(ctx.w_dtype), d_scores,
+                                                    ctx.renormalize, ctx.scaling_factor)
+        return d_logits, None, None, None, None, None, None, None, None
+
+
+class MI355XTopKRouter(_RouterBase):
+    """Softmax top-k router (Qwen3MoeTopKRouter.forward,
+    src/models/modeling_qwen3_moe.py:266-275): returns
+    (router_logits = softmax probs fp32 [T,E], weights fp32 [T,K], index [T,K]).
+
+    ``logit_offset`` (optional [E] fp32 attribute) is added to the logits
+    before the softmax; the skewed-routing benchmark config uses it."""
+
+    def __init__(self, config):
+        super().__init__(config)
+        self.logit_offset: torch.Tensor | None = None
+
+    def forward(self, hidden_states):
+        hidden_states = hidden_states.reshape(-1, self.hidden_dim)
+        logits = F.linear(hidden_states, self.weight)
+        return SoftmaxTopKFunction.apply(logits, self.top_k, bool(self.norm_topk_prob),
+                                         self.logit_offset)
+
+    @classmethod
+    def from_router(cls, old: nn.Module) -> "MI355XTopKRouter":
+        cfg = SimpleNamespace(num_experts_per_tok=old.top_k, num_experts=old.num_experts,
+                              norm_topk_prob=old.norm_topk_prob, hidden_size=old.hidden_dim)
+        new = cls(cfg)
+        new.weight = old.weight  # share the Parameter: optimizer state and ckpt keys unchanged
+        new.logit_offset = getattr(old, "logit_offset", None)
+        return new
+
+
+class MI355XDeepSeekRouter(_RouterBase):
+    """DeepSeek-V3 sigmoid + expert-bias router (src/models/router.py:73-155):
+    fp32 gating linear, sigmoid scores, biased (optionally group-limited)
+    top-k, unbiased renormalised weights (+1e-20) times topk_scaling_factor,
+    cast to the hidden dtype.  Keeps the reference's buffers:
+    ``expert_bias`` (persistent), ``local_tokens_per_expert`` (non-persistent,
+    incremented only when grad is enabled) and ``_last_top_k_idx``."""
+
+    def __init__(self, config):
+        super().__init__(config)
+        self.scaling_factor = getattr(config, "topk_scaling_factor", None)
+        self.num_groups = getattr(config, "num_groups", None)
+        self.group_topk = getattr(config, "group_topk", None)
+        self.register_buffer("expert_bias", torch.zeros(self.num_experts, dtype=torch.float32))
+        self.register_buffer("local_tokens_per_expert",
+                             torch.zeros(self.num_experts, dtype=torch.float32), persistent=False)
+        self._last_top_k_idx = None
+
+    def forward(self, hidden_states):
+        hidden_states = hidden_states.reshape(-1, self.hidden_dim)
+        logits = F.linear(hidden_states.float(), self.weight.float())
+        counting = torch.is_grad_enabled()
+        scores, w, idx = SigmoidTopKFunction.apply(
+            logits, self.expert_bias, self.top_k, bool(self.norm_topk_prob), self.scaling_factor,
+            self.num_groups, self.group_topk, hidden_states.dtype,
+            self.local_tokens_per_expert if counting else None)
+        self._last_top_k_idx = idx.detach()
+        return scores, w, idx
+
+    @classmethod
+    def from_router(cls, old: nn.Module) -> "MI355XDeepSeekRouter":
+        cfg = SimpleNamespace(num_experts_per_tok=old.top_k, num_experts=old.num_experts,
+                              norm_topk_prob=old.norm_topk_prob, hidden_size=old.hidden_dim,
+                              topk_scaling_factor=getattr(old, "scaling_factor", None),
+                              num_groups=getattr(old, "num_groups", None),
+                              group_topk=getattr(old, "group_topk", None))
+        new = cls(cfg)
+        new.weight = old.weight
+        new.expert_bias = old.expert_bias
+        new.local_tokens_per_expert = old.local_tokens_per_expert
+        new._last_top_k_idx = getattr(old, "_last_top_k_idx", None)
+        return new

@@ -1,0 +1,197 @@
+"""The drop-in boundary: the C ABI surface and the transformers plug-in.
+
+CPU tests: the library exports every symbol include/moe_amd.h declares, the
+ctypes prototypes match the header's parameter counts, the "mi355x" key
+registers in transformers' ExpertsInterface, install() swaps routers in place
+without changing state_dict keys, and CPU tensors are refused (no fallback).
+GPU tests: a tiny Qwen3MoeForCausalLM runs fwd+bwd through the HIP path, its
+MoE blocks match the oracle, and a bank shared by two routers (the reference's
+global bank) accumulates both calls' weight gradients.
+"""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+from types import SimpleNamespace
+
+import pytest
+import torch
+from torch import nn
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "moe_amd.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for m in re.finditer(r"\b(?:int|size_t|const char\*)\s+(moe_amd_\w+)\(([^)]*)\)", text):
+        args = m.group(2).strip()
+        out[m.group(1)] = 0 if args in ("", "void") else len(args.split(","))
+    return out
+
+
+def test_header_declares_entry_points():
+    decl = _declared()
+    assert len(decl) >= 17
+    assert "moe_amd_permute" in decl and "moe_amd_gemm_gate_up_swiglu" in decl
+
+
+def test_library_exports_every_declared_symbol(built_lib):
+    lib = ctypes.CDLL(str(built_lib))
+    for name in _declared():
+        assert hasattr(lib, name), f"{name} not exported"
+
+
+def test_ctypes_prototypes_match_header():
+    from moe_amd import _lib
+    decl = _declared()
+    assert set(decl) == set(_lib.SIGNATURES)
+    for name, n in decl.items():
+        assert len(_lib.SIGNATURES[name][1]) == n, name
+
+
+def test_abi_version_and_error_text(built_lib):
+    from moe_amd import _lib
+    lib = _lib.load()
+    assert lib.moe_amd_abi_version() == 1
+    # Argument validation runs on the host: no GPU needed to see the error path.
+    rc = lib.moe_amd_permute(None, 10, 0, None, 0, None, None, None, None, None, None)
+    assert rc == -1
+    assert "E=0" in _lib.last_error()
+    rc = lib.moe_amd_gemm_down(None, None, None, None, 16, 4, 100, 64, 1, None, None)
+    assert rc == -1 and "multiples of 64" in _lib.last_error()
+    rc = lib.moe_amd_gemm_down(None, None, None, None, 16, 4, 128, 64, 0, None, None)
+    assert rc == -6 and "bf16" in _lib.last_error()
+
+
+def _tiny_model():
+    from transformers import Qwen3MoeConfig, Qwen3MoeForCausalLM
+    cfg = Qwen3MoeConfig(vocab_size=256, hidden_size=128, intermediate_size=256,
+                         moe_intermediate_size=64, num_hidden_layers=2, num_attention_heads=2,
+                         num_key_value_heads=1, head_dim=64, num_experts=8,
+                         num_experts_per_tok=2, norm_topk_prob=True, decoder_sparse_step=1,
+                         max_position_embeddings=128)
+    torch.manual_seed(0)
+    m = Qwen3MoeForCausalLM(cfg)
+    with torch.no_grad():
+        for n, p in m.named_parameters():
+            if "experts" in n or "gate.weight" in n:
+                p.normal_(0, 0.02)
+    return m
+
+
+def test_register_and_install_swap_in_place():
+    from transformers.integrations.moe import ALL_EXPERTS_FUNCTIONS
+    from moe_amd import hf
+    from moe_amd.router import MI355XTopKRouter
+    m = _tiny_model()
+    keys = list(m.state_dict().keys())
+    w_before = m.model.layers[0].mlp.gate.weight
+    hf.install(m)
+    assert "mi355x" in ALL_EXPERTS_FUNCTIONS
+    assert m.config._experts_implementation == "mi355x"
+    assert m.model.layers[0].mlp.experts.config._experts_implementation == "mi355x"
+    assert isinstance(m.model.layers[1].mlp.gate, MI355XTopKRouter)
+    assert m.model.layers[0].mlp.gate.weight is w_before
+    assert list(m.state_dict().keys()) == keys
+    with pytest.raises(RuntimeError, match="GPU only"):
+        m(torch.randint(0, 256, (1, 8)))
+
+
+def test_deepseek_router_swap_keeps_buffers():
+    from transformers.models.qwen3_moe.modeling_qwen3_moe import Qwen3MoeTopKRouter
+    from moe_amd import hf
+    from moe_amd.router import MI355XDeepSeekRouter
+
+    class BiasRouter(Qwen3MoeTopKRouter):  # stands in for the reference's DeepSeekRouter
+        def __init__(self, config):
+            super().__init__(config)
+            self.scaling_factor = 2.5
+            self.num_groups = None
+            self.group_topk = None
+            self.register_buffer("expert_bias", torch.randn(config.num_experts))
+            self.register_buffer("local_tokens_per_expert", torch.zeros(config.num_experts),
+                                 persistent=False)
+
+    cfg = SimpleNamespace(num_experts_per_tok=4, num_experts=16, norm_topk_prob=True,
+                          hidden_size=64)
+    holder = nn.Module()
+    holder.gate = BiasRouter(cfg)
+    sd = holder.state_dict()
+    assert hf.swap_routers(holder) == 1
+    assert isinstance(holder.gate, MI355XDeepSeekRouter)
+    assert holder.gate.scaling_factor == 2.5
+    new_sd = holder.state_dict()
+    assert set(new_sd) == set(sd) == {"gate.weight", "gate.expert_bias"}
+    assert torch.equal(new_sd["gate.expert_bias"], sd["gate.expert_bias"])
+
+
+def test_unsupported_expert_variants_raise():
+    from moe_amd.experts import mi355x_experts_forward
+    fake = SimpleNamespace(has_gate=True, has_bias=True, is_transposed=False)
+    with pytest.raises(NotImplementedError):
+        mi355x_experts_forward(fake, None, None, None)
+
+
+# ------------------------------------------------------------------ GPU
+
+@pytest.mark.gpu
+def test_tiny_hf_model_runs_on_hip_path_and_matches_oracle():
+    from oracle import moe_oracle as O
+    from moe_amd import hf
+    m = _tiny_model().to("cuda", torch.bfloat16)
+    hf.install(m)
+    captured = []
+    blk = m.model.layers[1].mlp
+    blk.register_forward_hook(lambda mod, inp, out: captured.append((inp[0].detach(),
+                                                                     out.detach())))
+    ids = torch.randint(0, 256, (2, 32), device="cuda")
+    out = m(ids, labels=ids, output_router_logits=True)
+    assert torch.isfinite(out.loss)
+    assert len(out.router_logits) == 2 and out.router_logits[0].shape == (64, 8)
+    out.loss.backward()
+    assert blk.experts.gate_up_proj.grad is not None and blk.gate.weight.grad is not None
+    h, y = captured[0]
+    flat = h.reshape(-1, 128)
+    logits = torch.nn.functional.linear(flat, blk.gate.weight).cpu()
+    _, w, idx = O.softmax_router(logits, 2)
+    ref, _ = O.experts_forward(flat.cpu(), idx, w, blk.experts.gate_up_proj.detach().cpu(),
+                               blk.experts.down_proj.detach().cpu())
+    err = (y.reshape(-1, 128).double().cpu() - ref.double()).abs().max() / ref.abs().max()
+    assert err < 2e-2
+
+
+@pytest.mark.gpu
+def test_shared_bank_accumulates_gradients_across_layers():
+    """One expert bank used by two routers (GlobalMoEModel's global_experts,
+    src/models/global_moe.py:138): its dW is the sum of both calls'."""
+    from oracle import moe_oracle as O
+    from moe_amd.layer import moe_layer
+    g = torch.Generator().manual_seed(5)
+    T, H, E, K, I = 512, 256, 32, 4, 128
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    w1 = (torch.randn(E, 2 * I, H, generator=g) * 0.02).to(torch.bfloat16)
+    w2 = (torch.randn(E, H, I, generator=g) * 0.02).to(torch.bfloat16)
+    r = [(torch.randn(E, H, generator=g) * 0.02).to(torch.bfloat16) for _ in range(2)]
+    d = [torch.randn(T, H, generator=g).to(torch.bfloat16) for _ in range(2)]
+    w1d = w1.cuda().requires_grad_(True)
+    w2d = w2.cuda().requires_grad_(True)
+    for layer in range(2):
+        out, _, _, _ = moe_layer(x.cuda(), r[layer].cuda(), w1d, w2d, K)
+        out.backward(d[layer].cuda())
+    torch.cuda.synchronize()
+    acc1 = torch.zeros(E, 2 * I, H, dtype=torch.float64)
+    acc2 = torch.zeros(E, H, I, dtype=torch.float64)
+    for layer in range(2):
+        logits = torch.nn.functional.linear(x.cuda(), r[layer].cuda()).cpu()
+        _, w, idx = O.softmax_router(logits, K)
+        _, cache = O.experts_forward(x, idx, w, w1, w2)
+        _, _, dw1, dw2, _ = O.experts_backward(cache, x, w, w1, w2, d[layer])
+        acc1 += dw1.double()
+        acc2 += dw2.double()
+    e1 = (w1d.grad.double().cpu() - acc1).abs().max() / acc1.abs().max()
+    e2 = (w2d.grad.double().cpu() - acc2).abs().max() / acc2.abs().max()
+    assert e1 < 2e-2 and e2 < 2e-2
