@@ -163,7 +163,7 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
     if constexpr (MODE == G2F) { base = p.a0; ld = I; }
     else if constexpr (MODE == G2DX) { base = p.a0; ld = H; }
     else { base = p.a0; ld = I2; }
-    rsrc = make_rsrc(base + (int64_t)row0 * ld, (uint32_t)((row_end - row0) * ld * 2));
+    rsrc = make_rsrc(base + (int64_t)row0 * ld, (uint32_t)((int64_t)(row_end - row0) * ld * 2));
 #pragma unroll
     for (int q = 0; q < RPASS; ++q) {
       int r = min(drow + 32 * q, row_end - row0 - 1);
@@ -172,7 +172,7 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
   } else {
     // dW: row operand [rows of e][features], features = C rows.
     const int ld = (MODE == G2DW) ? H : I2;
-    rsrc = make_rsrc(p.a0 + (int64_t)kbeg * ld, (uint32_t)((kend - kbeg) * ld * 2));
+    rsrc = make_rsrc(p.a0 + (int64_t)kbeg * ld, (uint32_t)((int64_t)(kend - kbeg) * ld * 2));
     rstride = (uint32_t)ld * 2;
     roff[0] = (uint32_t)(kb * 8) * rstride + (uint32_t)(row0 + fb * 8) * 2;
   }
@@ -207,7 +207,7 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
     cstride = (uint32_t)H * 2;
     coff[0] = (uint32_t)(kb * 8) * cstride + (uint32_t)(ct * BC + fb * 8) * 2;
   } else if constexpr (MODE == G2DW) {
-    csrc = make_rsrc(p.a1 + (int64_t)kbeg * I, (uint32_t)((kend - kbeg) * I * 2));
+    csrc = make_rsrc(p.a1 + (int64_t)kbeg * I, (uint32_t)((int64_t)(kend - kbeg) * I * 2));
     cstride = (uint32_t)I * 2;
     coff[0] = (uint32_t)(kb * 8) * cstride + (uint32_t)(ct * BC + fb * 8) * 2;
   } else {  // G1DW: gathered hidden_states rows
@@ -469,7 +469,9 @@ int check_common(int64_t S, int E, int H, int I, int dtype, const char* who) {
   MOE_REQUIRE(H % 64 == 0 && I % 64 == 0, MOE_ERR_ARG,
               "%s: H=%d and I=%d must be multiples of 64", who, H, I);
   const int64_t widest = H > 2 * I ? H : 2 * (int64_t)I;
-  MOE_REQUIRE(S * widest * 2 < ((int64_t)1 << 31), MOE_ERR_UNSUPPORTED,
+  // Buffer descriptors address at most one expert's rows (<= S) with
+  // 32-bit byte offsets.
+  MOE_REQUIRE(S * widest * 2 < ((int64_t)1 << 32), MOE_ERR_UNSUPPORTED,
               "%s: S*max(H,2I) too large for 32-bit buffer offsets", who);
   MOE_REQUIRE((int64_t)E * H * 2 * I * 2 < ((int64_t)1 << 40), MOE_ERR_ARG, "%s: weights too large",
               who);

@@ -74,7 +74,7 @@ def test_forward_kernels_parity(T, H, E, K, I, skew, sent, wdt):
     assert _rel(out, out_ref) < TOL
     # act without the gate_up side output is identical
     _, act2 = ops.gemm_gate_up_swiglu(x.to(DEV), plan, w1.to(DEV), save_gate_up=False)
-    assert torch.equal(act2, act)
+    assert torch.equal(act2[:nv], act[:nv])  # sentinel rows are never written
 
 
 @pytest.mark.parametrize("T,H,E,K,I,skew,sent,wdt", CASES)
