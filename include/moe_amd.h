@@ -104,6 +104,9 @@ int moe_amd_router_sigmoid_topk_backward(const float* scores, const int64_t* top
 /* Workspace bytes moe_amd_permute() needs for S routed rows, E experts. */
 size_t moe_amd_permute_workspace_size(int64_t S, int E);
 
+/* Bytes of the GEMM tile plan moe_amd_permute() writes for S rows, E experts. */
+size_t moe_amd_tile_plan_size(int64_t S, int E);
+
 /* Counting sort of the flattened topk_index [S] by expert id.  Replaces the
  * sort / histc / cumsum of transformers/integrations/moe.py:389-403 (the
  * reference sort is unstable; this one is stable).  Outputs (int32):
@@ -112,30 +115,35 @@ size_t moe_amd_permute_workspace_size(int64_t S, int E);
  *                         owned by real experts (cumsum(counts)[-1])
  *   row_src [S]           sorted row r -> flat routed index t*K+k (perm)
  *   slot [S]              flat routed index -> sorted row (inverse perm)
- *   tile_starts [3*(E+1)] exclusive prefix of ceil(counts/BM) for the
- *                         row-tile heights BM = 64, 128, 256 (GEMM plan). */
+ *   tile_plan             16-byte aligned, moe_amd_tile_plan_size() bytes:
+ *                         int32 tile_starts[3][E+1] (exclusive prefix of
+ *                         ceil(counts/BM), BM = 64, 128, 256), then per BM
+ *                         an int4 table {expert, first row, end row, 0} of
+ *                         every row tile; the grouped GEMMs read it. */
 int moe_amd_permute(const int64_t* topk_index, int64_t S, int E, void* workspace,
                     size_t workspace_bytes, int32_t* counts, int32_t* offsets, int32_t* row_src,
-                    int32_t* slot, int32_t* tile_starts, void* stream);
+                    int32_t* slot, void* tile_plan, size_t tile_plan_bytes, void* stream);
 
 /* ------------------------------------------------------- grouped GEMMs */
 /* All GEMMs: bf16 operands (dtype = MOE_DTYPE_BF16), fp32 accumulation,
  * bf16 results; H and I must be multiples of 64; pointers 16-byte aligned.
- * The expert of each routed row is found from offsets / tile_starts on the
- * device, so empty and skewed experts cost no host synchronisation. */
+ * The expert of each row tile is read from the tile plan on the device, so
+ * empty and skewed experts cost no host synchronisation.  The kernels are
+ * persistent: one workgroup per compute unit walks a contiguous range of
+ * tiles per XCD. */
 
 /* gate_up = xs @ gate_up_proj[e]^T with xs[r] = hidden_states[row_src[r]/K],
  * then act = silu(gate) * up.  transformers/integrations/moe.py:439-447.
  * gate_up_out [S,2I] (may be NULL: inference), act_out [S,I]. */
 int moe_amd_gemm_gate_up_swiglu(const void* hidden_states, const int32_t* row_src, int top_k,
-                                const int32_t* offsets, const int32_t* tile_starts,
+                                const int32_t* offsets, const void* tile_plan,
                                 const void* gate_up_proj, int64_t T, int64_t S, int E, int H,
                                 int I, int dtype, void* gate_up_out, void* act_out,
                                 void* stream);
 
 /* y = act @ down_proj[e]^T.  transformers/integrations/moe.py:449-459.
  * y_out [S,H]. */
-int moe_amd_gemm_down(const void* act, const int32_t* offsets, const int32_t* tile_starts,
+int moe_amd_gemm_down(const void* act, const int32_t* offsets, const void* tile_plan,
                       const void* down_proj, int64_t S, int E, int H, int I, int dtype,
                       void* y_out, void* stream);
 
@@ -143,7 +151,7 @@ int moe_amd_gemm_down(const void* act, const int32_t* offsets, const int32_t* ti
  * d_act = dy @ down_proj[e]; (d_gate, d_up) from gate_up; writes
  * d_gate_up [S,2I].  Autograd of integrations/moe.py:447,457 (formula :226-242). */
 int moe_amd_gemm_down_backward_dx_dswiglu(const void* dy, const int32_t* offsets,
-                                          const int32_t* tile_starts, const void* down_proj,
+                                          const void* tile_plan, const void* down_proj,
                                           const void* gate_up, int64_t S, int E, int H, int I,
                                           int dtype, void* d_gate_up, void* stream);
 
@@ -154,7 +162,7 @@ int moe_amd_gemm_down_backward_dw(const void* dy, const void* act, const int32_t
 
 /* d_xs = d_gate_up @ gate_up_proj[e]  ([S,H]). */
 int moe_amd_gemm_gate_up_backward_dx(const void* d_gate_up, const int32_t* offsets,
-                                     const int32_t* tile_starts, const void* gate_up_proj,
+                                     const void* tile_plan, const void* gate_up_proj,
                                      int64_t S, int E, int H, int I, int dtype, void* d_xs,
                                      void* stream);
 

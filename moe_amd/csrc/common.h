@@ -33,6 +33,22 @@ int check_launch(const char* what);
 
 static inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
+// ---- GEMM tile plan (written by the permutation, read by the GEMMs) -----
+// int32 tile_starts[3][E+1]: exclusive prefix of ceil(count_e / BM) for the
+// row-tile heights BM = 64, 128, 256; then, 16-byte aligned, for each BM an
+// int4 table info[ceil(S/BM) + E] = {expert, first row, end row, 0} of
+// every row tile in expert order.
+constexpr int kTileSizes[3] = {64, 128, 256};
+static inline int64_t plan_max_tiles(int64_t S, int E, int b) {
+  return (S + kTileSizes[b] - 1) / kTileSizes[b] + E;
+}
+static inline size_t plan_info_offset(int64_t S, int E, int b) {
+  size_t off = align_up((size_t)3 * (E + 1) * sizeof(int), 16);
+  for (int i = 0; i < b; ++i) off += 16 * (size_t)plan_max_tiles(S, E, i);
+  return off;
+}
+static inline size_t plan_bytes(int64_t S, int E) { return plan_info_offset(S, E, 3); }
+
 // ---- bf16 helpers -------------------------------------------------------
 // Conversions go through clang's __bf16 type, which rounds to nearest-even
 // (the same rounding torch applies when it stores an fp32 result as bf16).

@@ -19,7 +19,6 @@ namespace {
 
 constexpr int kChunk = 256;        // entries per wave in P1/P3
 constexpr int kWaves = 4;          // waves per block in P1/P3
-constexpr int kTileSizes[MOE_NUM_TILE_SIZES] = {64, 128, 256};
 
 __device__ __forceinline__ int bin_of(int64_t id, int E) {
   return (id >= 0 && id < E) ? (int)id : E;
@@ -125,6 +124,23 @@ __global__ __launch_bounds__(1024) void finalize_kernel(const int* __restrict__ 
   }
 }
 
+// Grid (E, 3): fills the row-tile table of expert blockIdx.x for tile height
+// kTileSizes[blockIdx.y].
+__global__ __launch_bounds__(64) void tile_info_kernel(const int* __restrict__ offsets,
+                                                       const int* __restrict__ tile_starts,
+                                                       int E, int4* __restrict__ info0,
+                                                       int4* __restrict__ info1,
+                                                       int4* __restrict__ info2) {
+  const int e = blockIdx.x, b = blockIdx.y;
+  const int bm = kTileSizes[b];
+  int4* info = b == 0 ? info0 : (b == 1 ? info1 : info2);
+  const int* ts = tile_starts + b * (E + 1);
+  const int t0 = ts[e], t1 = ts[e + 1];
+  const int r0 = offsets[e], r1 = offsets[e + 1];
+  for (int t = t0 + (int)threadIdx.x; t < t1; t += 64)
+    info[t] = make_int4(e, r0 + (t - t0) * bm, r1, 0);
+}
+
 __global__ __launch_bounds__(64 * kWaves) void scatter_kernel(
     const int64_t* __restrict__ ids, int64_t S, int E, int64_t nch,
     const int* __restrict__ chunk_off, const int* __restrict__ offsets,
@@ -183,14 +199,22 @@ extern "C" size_t moe_amd_permute_workspace_size(int64_t S, int E) {
   return permute_ws_bytes(S, E);
 }
 
+extern "C" size_t moe_amd_tile_plan_size(int64_t S, int E) {
+  if (S < 0 || E < 1) return 0;
+  return plan_bytes(S, E);
+}
+
 extern "C" int moe_amd_permute(const int64_t* topk_index, int64_t S, int E, void* workspace,
                                size_t workspace_bytes, int32_t* counts, int32_t* offsets,
-                               int32_t* row_src, int32_t* slot, int32_t* tile_starts,
-                               void* stream) {
+                               int32_t* row_src, int32_t* slot, void* tile_plan,
+                               size_t tile_plan_bytes, void* stream) {
   MOE_REQUIRE(S >= 0 && S < (int64_t)1 << 31, MOE_ERR_ARG, "permute: S=%lld out of range",
               (long long)S);
   MOE_REQUIRE(E >= 1 && E <= 16384, MOE_ERR_ARG, "permute: E=%d out of range", E);
-  MOE_REQUIRE(counts && offsets && tile_starts, MOE_ERR_ARG, "permute: null output");
+  MOE_REQUIRE(counts && offsets && tile_plan, MOE_ERR_ARG, "permute: null output");
+  MOE_REQUIRE(tile_plan_bytes >= plan_bytes(S, E) && ((uintptr_t)tile_plan & 15) == 0,
+              MOE_ERR_WORKSPACE, "permute: tile plan needs %zu bytes, 16-byte aligned",
+              plan_bytes(S, E));
   MOE_REQUIRE(S == 0 || (topk_index && row_src && slot), MOE_ERR_ARG, "permute: null pointer");
   const size_t need = permute_ws_bytes(S, E);
   MOE_REQUIRE(workspace && workspace_bytes >= need, MOE_ERR_WORKSPACE,
@@ -206,7 +230,13 @@ extern "C" int moe_amd_permute(const int64_t* topk_index, int64_t S, int E, void
     hist_kernel<<<blocks, 64 * kWaves, lds, st>>>(topk_index, S, E, nch, chunk_hist);
     chunk_scan_kernel<<<E + 1, 256, 0, st>>>(chunk_hist, nch, totals);
   }
+  int* tile_starts = (int*)tile_plan;
   finalize_kernel<<<1, 1024, 0, st>>>(totals, nch > 0 ? 1 : 0, E, counts, offsets, tile_starts);
+  char* pb = (char*)tile_plan;
+  tile_info_kernel<<<dim3(E, 3), 64, 0, st>>>(offsets, tile_starts, E,
+                                              (int4*)(pb + plan_info_offset(S, E, 0)),
+                                              (int4*)(pb + plan_info_offset(S, E, 1)),
+                                              (int4*)(pb + plan_info_offset(S, E, 2)));
   if (nch > 0) {
     const int blocks = (int)((nch + kWaves - 1) / kWaves);
     scatter_kernel<<<blocks, 64 * kWaves, lds, st>>>(topk_index, S, E, nch, chunk_hist,

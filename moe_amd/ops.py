@@ -158,12 +158,14 @@ class RoutingPlan:
 
     counts [E], offsets [E+1] (exclusive; offsets[E] = rows of real experts),
     row_src [S] (sorted row -> flat t*K+k), slot [S] (flat -> sorted row),
-    tile_starts [3, E+1] (row-tile prefixes for BM = 64/128/256)."""
+    tile_plan (bytes; starts with the int32 row-tile prefixes [3, E+1] for
+    BM = 64/128/256, followed by the per-tile {expert, first row, end row}
+    tables the grouped GEMMs read)."""
     counts: torch.Tensor
     offsets: torch.Tensor
     row_src: torch.Tensor
     slot: torch.Tensor
-    tile_starts: torch.Tensor
+    tile_plan: torch.Tensor
     num_experts: int
     top_k: int
     num_tokens: int
@@ -171,6 +173,11 @@ class RoutingPlan:
     @property
     def num_rows(self) -> int:
         return self.row_src.numel()
+
+    @property
+    def tile_starts(self) -> torch.Tensor:
+        E = self.num_experts
+        return self.tile_plan[: 3 * (E + 1) * 4].view(torch.int32).view(3, E + 1)
 
 
 def permute(topk_index: torch.Tensor, num_experts: int) -> RoutingPlan:
@@ -190,11 +197,12 @@ def permute(topk_index: torch.Tensor, num_experts: int) -> RoutingPlan:
     offsets = torch.empty(E + 1, device=dev, dtype=torch.int32)
     row_src = torch.empty(S, device=dev, dtype=torch.int32)
     slot = torch.empty(S, device=dev, dtype=torch.int32)
-    tile_starts = torch.empty(_lib.NUM_TILE_SIZES, E + 1, device=dev, dtype=torch.int32)
+    plan_bytes = int(lib.moe_amd_tile_plan_size(S, E))
+    tile_plan = torch.empty(plan_bytes, device=dev, dtype=torch.uint8)
     _call("moe_amd_permute", topk_index.data_ptr(), S, E, ws.data_ptr(), ws.numel(),
           counts.data_ptr(), offsets.data_ptr(), row_src.data_ptr(), slot.data_ptr(),
-          tile_starts.data_ptr(), _stream(topk_index))
-    return RoutingPlan(counts, offsets, row_src, slot, tile_starts, E, K, T)
+          tile_plan.data_ptr(), plan_bytes, _stream(topk_index))
+    return RoutingPlan(counts, offsets, row_src, slot, tile_plan, E, K, T)
 
 
 # --------------------------------------------------------- grouped GEMMs
@@ -209,7 +217,7 @@ def gemm_gate_up_swiglu(x: torch.Tensor, plan: RoutingPlan, gate_up_proj: torch.
     act = torch.empty(S, I, device=x.device, dtype=x.dtype)
     gu = torch.empty(S, I2, device=x.device, dtype=x.dtype) if save_gate_up else None
     _call("moe_amd_gemm_gate_up_swiglu", x.data_ptr(), plan.row_src.data_ptr(), plan.top_k,
-          plan.offsets.data_ptr(), plan.tile_starts.data_ptr(), gate_up_proj.data_ptr(),
+          plan.offsets.data_ptr(), plan.tile_plan.data_ptr(), gate_up_proj.data_ptr(),
           plan.num_tokens, S, E, H, I, _dtype_code(x.dtype), _ptr(gu), act.data_ptr(),
           _stream(x))
     return gu, act
@@ -221,7 +229,7 @@ def gemm_down(act: torch.Tensor, plan: RoutingPlan, down_proj: torch.Tensor) -> 
     S = plan.num_rows
     y = torch.empty(S, H, device=act.device, dtype=act.dtype)
     _call("moe_amd_gemm_down", act.data_ptr(), plan.offsets.data_ptr(),
-          plan.tile_starts.data_ptr(), down_proj.data_ptr(), S, E, H, I,
+          plan.tile_plan.data_ptr(), down_proj.data_ptr(), S, E, H, I,
           _dtype_code(act.dtype), y.data_ptr(), _stream(act))
     return y
 
@@ -232,7 +240,7 @@ def gemm_down_backward_dx_dswiglu(dy, plan: RoutingPlan, down_proj, gate_up):
     S = plan.num_rows
     dgu = torch.empty(S, 2 * I, device=dy.device, dtype=dy.dtype)
     _call("moe_amd_gemm_down_backward_dx_dswiglu", dy.data_ptr(), plan.offsets.data_ptr(),
-          plan.tile_starts.data_ptr(), down_proj.data_ptr(), gate_up.data_ptr(), S, E, H, I,
+          plan.tile_plan.data_ptr(), down_proj.data_ptr(), gate_up.data_ptr(), S, E, H, I,
           _dtype_code(dy.dtype), dgu.data_ptr(), _stream(dy))
     return dgu
 
@@ -254,7 +262,7 @@ def gemm_gate_up_backward_dx(dgu, plan: RoutingPlan, gate_up_proj):
     S = plan.num_rows
     dxs = torch.empty(S, H, device=dgu.device, dtype=dgu.dtype)
     _call("moe_amd_gemm_gate_up_backward_dx", dgu.data_ptr(), plan.offsets.data_ptr(),
-          plan.tile_starts.data_ptr(), gate_up_proj.data_ptr(), S, E, H, I2 // 2,
+          plan.tile_plan.data_ptr(), gate_up_proj.data_ptr(), S, E, H, I2 // 2,
           _dtype_code(dgu.dtype), dxs.data_ptr(), _stream(dgu))
     return dxs
 

@@ -35,7 +35,7 @@ def _declared():
 
 def test_header_declares_entry_points():
     decl = _declared()
-    assert len(decl) >= 17
+    assert len(decl) >= 18
     assert "moe_amd_permute" in decl and "moe_amd_gemm_gate_up_swiglu" in decl
 
 
@@ -58,7 +58,7 @@ def test_abi_version_and_error_text(built_lib):
     lib = _lib.load()
     assert lib.moe_amd_abi_version() == 1
     # Argument validation runs on the host: no GPU needed to see the error path.
-    rc = lib.moe_amd_permute(None, 10, 0, None, 0, None, None, None, None, None, None)
+    rc = lib.moe_amd_permute(None, 10, 0, None, 0, None, None, None, None, None, 0, None)
     assert rc == -1
     assert "E=0" in _lib.last_error()
     rc = lib.moe_amd_gemm_down(None, None, None, None, 16, 4, 100, 64, 1, None, None)

@@ -67,3 +67,24 @@ def test_permute_zero_tokens():
     assert plan.offsets.cpu().tolist() == [0] * 17
     assert plan.counts.cpu().tolist() == [0] * 16
     assert plan.tile_starts.cpu().sum().item() == 0
+
+
+@pytest.mark.parametrize("T,E,K", [(4096, 128, 8), (1001, 64, 3), (512, 1792, 8)])
+def test_tile_plan_tables(T, E, K):
+    """The {expert, first row, end row} table of every row tile, per tile height."""
+    idx = _routing(T, E, K, 5 + E)
+    plan = ops.permute(idx.to(DEV), E)
+    torch.cuda.synchronize()
+    ref = O.permute(idx, E)
+    raw = plan.tile_plan.cpu().numpy()
+    S = T * K
+    base = (3 * (E + 1) * 4 + 15) // 16 * 16
+    for b, bm in enumerate(O.TILE_SIZES):
+        ntile = int(ref.tile_starts[b, E])
+        info = raw[base: base + 16 * ntile].view(np.int32).reshape(ntile, 4)[:, :3]
+        exp = []
+        for e in range(E):
+            lo, hi = int(ref.offsets[e]), int(ref.offsets[e + 1])
+            exp += [(e, r, hi) for r in range(lo, hi, bm)]
+        assert info.tolist() == [list(x) for x in exp]
+        base += 16 * ((S + bm - 1) // bm + E)
