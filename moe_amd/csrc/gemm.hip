@@ -14,14 +14,23 @@
 //   G2DW  d_down_proj[e]         H                   I               rows of e
 //   G1DW  d_gate_up_proj[e]      2I                  H               rows of e
 //
-// Operands are staged through LDS in [row][64 k] bf16 tiles, 128-byte rows,
-// with 16-byte chunks XOR-swizzled by (row >> 1) & 7 so that fragment reads
-// and both kinds of tile writes are bank-conflict free.  Operands whose
-// memory layout is k-major ("transposed": weights in the dX GEMMs, every
-// operand of the dW GEMMs) are loaded as 8x8 bf16 blocks and transposed in
-// registers with v_perm before the LDS write.  Global loads are raw buffer
-// loads: reads past a tensor's extent return zero, which both guards the
-// tails and zero-fills the ragged k range of the dW GEMMs.
+// Data path: global -> LDS by DMA (gfx950 `buffer_load_dwordx4 ... lds`: lane
+// L of a wave instruction writes 16 bytes at M0 + 16*L), so operands cost no
+// VGPRs and no ds_write.  LDS holds 4 stages of BK = 32; while stage kt is
+// consumed, stages kt+1..kt+3 are in flight, each wave counting its own DMA
+// with s_waitcnt vmcnt before the stage barrier.  Two LDS layouts:
+//   * k-contiguous operands (activation rows, the forward weights) are kept
+//     as [feature][32 k] (64-byte rows, 16-byte chunks XOR-swizzled by
+//     (feature >> 2) & 3) and read with ds_read_b128;
+//   * k-major operands (the weights of the dX GEMMs, every operand of the dW
+//     GEMMs) are copied as they lie, [32 k][features] (16-byte chunks
+//     swizzled by (k & 3) << 2), and read with ds_read_b64_tr_b16, whose
+//     16-lane transpose turns four 8-byte row reads into one lane's four
+//     consecutive k values -- no register transposes.
+// The swizzles make every DMA block a contiguous 1 KB and every fragment
+// read bank-conflict free.  Global reads are raw buffer loads: reads past a
+// tensor's extent return zero, which guards tails and zero-fills the ragged
+// k range of the dW GEMMs.
 //
 // Scheduling: the kernel is persistent (one workgroup per CU).  The tile
 // space -- (row tile, column tile) for the token-grouped modes, (expert, row
@@ -31,8 +40,7 @@
 // weights and rows in that XCD's L2.  A token-grouped tile reads its
 // {expert, first row, end row} from the tile plan written by the
 // permutation on the device: skewed and empty experts need no host round
-// trip.  The first k-stage of a workgroup's next tile is loaded before the
-// current tile's epilogue, hiding its latency behind the output writes.
+// trip.
 //
 // Epilogue: accumulators are rounded to bf16 into an LDS staging tile, then
 // written out row by row with 16-byte lanes (full-line stores), applying the
@@ -45,10 +53,11 @@
 namespace moe {
 namespace {
 
-constexpr int BK = 64;    // k per LDS stage
-constexpr int BC = 256;   // output columns per workgroup
-constexpr int NTHR = 256; // 4 waves
-constexpr int SROW = 260; // bf16 per row of the epilogue staging tile (520 B: conflict-free)
+constexpr int BK = 32;     // k per LDS stage
+constexpr int NSTAGE = 4;  // LDS stages: one consumed, three in flight
+constexpr int BC = 256;    // output columns per workgroup
+constexpr int NTHR = 256;  // 4 waves
+constexpr int SROW = 260;  // bf16 per row of the epilogue staging tile (520 B: conflict-free)
 
 enum Mode { G1F = 0, G2F = 1, G2DX = 2, G1DX = 3, G2DW = 4, G1DW = 5 };
 
@@ -72,49 +81,49 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
                                            0x00020000);
 }
-__device__ __forceinline__ u32x4 bload(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
-}
 
 constexpr uint32_t kOOB = 0x80000000u;  // offset that always reads as zero
 
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4_t;
 
-// Writes an 8x8 bf16 block, transposed, into a [row][64] LDS tile.
-// v[r] holds 8 consecutive features of k-row kb*8+r; feature c of the block
-// goes to tile row fb*8+c as 8 consecutive k values (16 bytes, chunk kb).
-// Odd feature blocks emit their rows in pair-swapped order (c ^ 1) so that
-// the 16 lanes of one LDS write phase cover both row parities (no bank
-// conflicts); the swap is folded into the v_perm byte selector, so there is
-// no data-dependent register selection.
-__device__ __forceinline__ void store_transposed(bf16* tile, const u32x4 (&v)[8], int fb, int kb) {
-  const int odd = fb & 1;
-  const uint32_t sel_a = odd ? 0x07060302u : 0x05040100u;  // feature 2q + odd
-  const uint32_t sel_b = odd ? 0x05040100u : 0x07060302u;  // feature 2q + 1 - odd
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    u32x4 a, b;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      a[j] = __builtin_amdgcn_perm(v[2 * j + 1][q], v[2 * j][q], sel_a);
-      b[j] = __builtin_amdgcn_perm(v[2 * j + 1][q], v[2 * j][q], sel_b);
-    }
-    const int row_a = fb * 8 + 2 * q + odd;
-    const int row_b = row_a ^ 1;
-    const int chunk = (kb ^ ((odd * 4 + q) & 7)) << 3;  // swizzle (row >> 1) & 7
-    *(u32x4*)(tile + row_a * 64 + chunk) = a;
-    *(u32x4*)(tile + row_b * 64 + chunk) = b;
-  }
+// 16-byte DMA of one lane into LDS (lane L lands at lds + 16*L).
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, void* lds) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)lds, 16, voff, 0, 0, 0);
+}
+
+// s_waitcnt encodings (gfx9 family): vmcnt in [3:0]+[15:14], lgkmcnt [11:8].
+constexpr int vmcnt_imm(int n) { return (n & 15) | (7 << 4) | (15 << 8) | (((n >> 4) & 3) << 14); }
+#define WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(vmcnt_imm(n))
+
+// One MFMA fragment (8 consecutive k of one feature) from a k-major stage
+// region: two transpose reads, k 0..3 and k 4..7.
+__device__ __forceinline__ bf16x8 tr_frag(const bf16* p0, const bf16* p1) {
+  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)p0);
+  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)p1);
+  const s16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(bf16x8, v);
 }
 
 template <int MODE, int BR>
 __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
-  constexpr bool TOKEN = MODE <= G1DX;          // rows = routed rows of one expert
-  constexpr bool COL_T = !(MODE == G1F || MODE == G2F);
-  constexpr int WR = BR / 2;                    // rows per wave
-  constexpr int TJ = WR / 32;                   // MFMA row sub-tiles per wave
-  constexpr int TI = 4;                         // MFMA col sub-tiles per wave (128 cols)
-  constexpr int RPASS = BR / 32;                // direct row-loader passes
-  constexpr int STAGE = (BC + BR) * BK;         // bf16 elements per LDS stage
+  constexpr bool TOKEN = MODE <= G1DX;                  // rows = routed rows of one expert
+  constexpr bool COL_KM = !(MODE == G1F || MODE == G2F);  // column operand k-major in memory
+  constexpr bool ROW_KM = !TOKEN;                       // row operand k-major (dW)
+  constexpr int WR = BR / 2;                            // rows per wave
+  constexpr int TJ = WR / 32;                           // MFMA row sub-tiles per wave
+  constexpr int TI = 4;                                 // MFMA col sub-tiles per wave (128 cols)
+  constexpr int CREG = BC * BK * 2;                     // bytes of the column region per stage
+  constexpr int RREG = BR * BK * 2;                     // bytes of the row region per stage
+  constexpr int STAGE_B = CREG + RREG;
+  constexpr int CBLK = CREG / 1024, RBLK = RREG / 1024; // 1 KB DMA blocks per region
+  constexpr int BPW = (CBLK + RBLK) / 4;                // DMA blocks per wave per stage
+  constexpr int RPW = BPW - CBLK / 4;                   // ... of which in the row region
+  constexpr int NTOK = (MODE == G1DW) ? CBLK / 4 : 0;   // gathered-row index loads per stage
+  constexpr int PER = BPW + NTOK;                       // vector-memory ops per stage issue
+  static_assert((CBLK + RBLK) % 4 == 0 && CBLK % 4 == 0, "DMA blocks per wave");
   static_assert(TOKEN || BR == 256, "dW modes use 256-row tiles");
 
   extern __shared__ __attribute__((aligned(16))) bf16 smem[];
@@ -172,165 +181,186 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
     return d;
   };
 
-  // ---------------------------------------------------------------- loaders
-  // Direct loader geometry: 16-byte chunk (t & 7) of tile row (t >> 3) + 32*pass.
-  const int dchunk = tid & 7, drow = tid >> 3;
-  const int dswz = (dchunk ^ ((drow >> 1) & 7)) << 3;
-  // Transposed loader geometry: k block kb (8 k rows), feature block fb (8 features).
-  const int kb = tid & 7, fb = tid >> 3;
+  // ------------------------------------------------------- DMA geometry
+  // Wave w fills the 1 KB blocks w, w+4, w+8, ... of each stage: blocks
+  // 0..CBLK-1 hold the column operand, the rest the row operand.  Within a
+  // block of a k-contiguous region, lane L carries feature 16*blk + L/4 and
+  // physical chunk L&3 (logical chunk (L&3) ^ ((feature>>2)&3)); within a
+  // block of a k-major region it carries k row 2*blk + L/32 and physical
+  // chunk L&31 (logical chunk (L&31) ^ ((k&3)<<2), 8 features per chunk).
+  auto kc_feature = [&](int blk) { return blk * 16 + (lane >> 2); };
+  auto kc_chunk = [&](int f) { return (lane & 3) ^ ((f >> 2) & 3); };
+  auto km_krow = [&](int blk) { return blk * 2 + (lane >> 5); };
+  auto km_chunk = [&](int k) { return (lane & 31) ^ ((k & 3) << 2); };
 
-  // Per-tile source descriptors (uniform parts live in SGPRs).
-  struct Src {
-    __amdgpu_buffer_rsrc_t r, c;
-    uint32_t roff[TOKEN ? RPASS : 1];
-    uint32_t coff[COL_T ? 1 : 8];
-    uint32_t rstride, cstride;
-    int kbeg, kend, ct;
-  };
-  auto setup = [&](const Tile& d, Src& s) {
-    s.kbeg = d.kbeg;
-    s.kend = d.kend;
-    s.ct = d.ct;
-    s.rstride = s.cstride = 0;
-    // Row operand.
-    if constexpr (MODE == G1F) {
-      s.r = make_rsrc(p.x, (uint32_t)(p.T * H * 2));
-#pragma unroll
-      for (int q = 0; q < RPASS; ++q) {
-        const int r = min(d.row0 + drow + 32 * q, d.row_end - 1);
-        const int tok = p.row_src[r] / p.topk;
-        s.roff[q] = (uint32_t)tok * (uint32_t)(H * 2) + dchunk * 16;
-      }
-    } else if constexpr (TOKEN) {
-      const int ld = (MODE == G2F) ? I : (MODE == G2DX ? H : I2);
-      s.r = make_rsrc(p.a0 + (int64_t)d.row0 * ld,
-                      (uint32_t)((int64_t)(d.row_end - d.row0) * ld * 2));
-#pragma unroll
-      for (int q = 0; q < RPASS; ++q) {
-        const int r = min(drow + 32 * q, d.row_end - d.row0 - 1);
-        s.roff[q] = (uint32_t)r * (uint32_t)(ld * 2) + dchunk * 16;
-      }
-    } else {
-      // dW: row operand [rows of e][features], features = C rows.
-      const int ld = (MODE == G2DW) ? H : I2;
-      s.r = make_rsrc(p.a0 + (int64_t)d.kbeg * ld,
-                      (uint32_t)((int64_t)(d.kend - d.kbeg) * ld * 2));
-      s.rstride = (uint32_t)ld * 2;
-      s.roff[0] = (uint32_t)(kb * 8) * s.rstride + (uint32_t)(d.row0 + fb * 8) * 2;
-    }
+  __amdgpu_buffer_rsrc_t csrc, rsrc, isrc;
+  uint32_t coff[CBLK / 4];   // byte offsets of this lane's column blocks at stage 0
+  uint32_t roff[RPW > 0 ? RPW : 1];
+  uint32_t cstep = 0, rstep = 0;  // byte advance per stage
+  // G1DW: byte offsets of the gathered x rows, rotated through three stages.
+  uint32_t tokA[NTOK > 0 ? NTOK : 1], tokB[NTOK > 0 ? NTOK : 1];
+  int ctile = 0, cfeat0 = 0, kb_cur = 0, ke_cur = 0;
+
+  auto setup = [&](const Tile& d) {
+    ctile = d.ct;
+    kb_cur = d.kbeg;
+    ke_cur = d.kend;
     // Column operand.
     if constexpr (MODE == G1F) {
-      s.c = make_rsrc(p.w + (int64_t)d.e * I2 * H, (uint32_t)(I2 * H * 2));
+      csrc = make_rsrc(p.w + (int64_t)d.e * I2 * H, (uint32_t)(I2 * H * 2));
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const int c = drow + 32 * q;  // tile column 0..255: [gate 64 | up 64] per wave column
-        const int lc = c & 127;
-        const int f = d.ct * 128 + (c >> 7) * 64 + (lc & 63);
-        const int wrow = (lc < 64) ? f : I + f;
-        s.coff[q] = (uint32_t)wrow * (uint32_t)(H * 2) + dchunk * 16;
+      for (int i = 0; i < CBLK / 4; ++i) {
+        const int f = kc_feature(wid + 4 * i);  // tile column: [gate 64 | up 64] per wave column
+        const int lc = f & 127;
+        const int feat = d.ct * 128 + (f >> 7) * 64 + (lc & 63);
+        const int wrow = (lc < 64) ? feat : I + feat;
+        coff[i] = (uint32_t)wrow * (uint32_t)(H * 2) + kc_chunk(f) * 16;
       }
+      cstep = BK * 2;
     } else if constexpr (MODE == G2F) {
-      s.c = make_rsrc(p.w + (int64_t)d.e * H * I, (uint32_t)(H * I * 2));
+      csrc = make_rsrc(p.w + (int64_t)d.e * H * I, (uint32_t)(H * I * 2));
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const int wrow = d.ct * BC + drow + 32 * q;
-        s.coff[q] = wrow < H ? (uint32_t)wrow * (uint32_t)(I * 2) + dchunk * 16 : kOOB;
+      for (int i = 0; i < CBLK / 4; ++i) {
+        const int f = kc_feature(wid + 4 * i);
+        const int wrow = d.ct * BC + f;
+        coff[i] = wrow < H ? (uint32_t)wrow * (uint32_t)(I * 2) + kc_chunk(f) * 16 : kOOB;
       }
-    } else if constexpr (MODE == G2DX) {
-      s.c = make_rsrc(p.w + (int64_t)d.e * H * I, (uint32_t)(H * I * 2));
-      s.cstride = (uint32_t)I * 2;
-      s.coff[0] = (uint32_t)(kb * 8) * s.cstride + (uint32_t)(d.ct * BC + fb * 8) * 2;
-    } else if constexpr (MODE == G1DX) {
-      s.c = make_rsrc(p.w + (int64_t)d.e * I2 * H, (uint32_t)(I2 * H * 2));
-      s.cstride = (uint32_t)H * 2;
-      s.coff[0] = (uint32_t)(kb * 8) * s.cstride + (uint32_t)(d.ct * BC + fb * 8) * 2;
-    } else if constexpr (MODE == G2DW) {
-      s.c = make_rsrc(p.a1 + (int64_t)d.kbeg * I, (uint32_t)((int64_t)(d.kend - d.kbeg) * I * 2));
-      s.cstride = (uint32_t)I * 2;
-      s.coff[0] = (uint32_t)(kb * 8) * s.cstride + (uint32_t)(d.ct * BC + fb * 8) * 2;
-    } else {  // G1DW: gathered hidden_states rows
-      s.c = make_rsrc(p.x, (uint32_t)(p.T * H * 2));
-      s.coff[0] = 0;
+      cstep = BK * 2;
+    } else {
+      // k-major column operand: rows of k, features contiguous.
+      int ld;
+      if constexpr (MODE == G2DX) {
+        csrc = make_rsrc(p.w + (int64_t)d.e * H * I, (uint32_t)(H * I * 2));
+        ld = I;
+      } else if constexpr (MODE == G1DX) {
+        csrc = make_rsrc(p.w + (int64_t)d.e * I2 * H, (uint32_t)(I2 * H * 2));
+        ld = H;
+      } else if constexpr (MODE == G2DW) {
+        csrc = make_rsrc(p.a1 + (int64_t)d.kbeg * I,
+                         (uint32_t)((int64_t)(d.kend - d.kbeg) * I * 2));
+        ld = I;
+      } else {  // G1DW: rows of hidden_states gathered through row_src
+        csrc = make_rsrc(p.x, (uint32_t)(p.T * H * 2));
+        ld = H;
+      }
+      cfeat0 = d.ct * BC;
+#pragma unroll
+      for (int i = 0; i < CBLK / 4; ++i) {
+        const int k = km_krow(wid + 4 * i);
+        const uint32_t fb = (uint32_t)(cfeat0 + km_chunk(k) * 8) * 2;
+        coff[i] = (MODE == G1DW) ? fb : (uint32_t)k * (uint32_t)(ld * 2) + fb;
+      }
+      cstep = (MODE == G1DW) ? 0 : (uint32_t)BK * ld * 2;
+    }
+    // Row operand.
+    if constexpr (MODE == G1F) {
+      rsrc = make_rsrc(p.x, (uint32_t)(p.T * H * 2));
+#pragma unroll
+      for (int i = 0; i < RPW; ++i) {
+        const int f = kc_feature(wid + 4 * i);  // row-region block index wid + 4*i
+        const int r = min(d.row0 + f, d.row_end - 1);
+        const int tok = p.row_src[r] / p.topk;
+        roff[i] = (uint32_t)tok * (uint32_t)(H * 2) + kc_chunk(f) * 16;
+      }
+      rstep = BK * 2;
+    } else if constexpr (TOKEN) {
+      const int ld = (MODE == G2F) ? I : (MODE == G2DX ? H : I2);
+      rsrc = make_rsrc(p.a0 + (int64_t)d.row0 * ld,
+                       (uint32_t)((int64_t)(d.row_end - d.row0) * ld * 2));
+#pragma unroll
+      for (int i = 0; i < RPW; ++i) {
+        const int f = kc_feature(wid + 4 * i);
+        const int r = min(f, d.row_end - d.row0 - 1);
+        roff[i] = (uint32_t)r * (uint32_t)(ld * 2) + kc_chunk(f) * 16;
+      }
+      rstep = BK * 2;
+    } else {
+      const int ld = (MODE == G2DW) ? H : I2;
+      rsrc = make_rsrc(p.a0 + (int64_t)d.kbeg * ld,
+                       (uint32_t)((int64_t)(d.kend - d.kbeg) * ld * 2));
+#pragma unroll
+      for (int i = 0; i < RPW; ++i) {
+        const int k = km_krow(wid + 4 * i);
+        roff[i] = (uint32_t)k * (uint32_t)(ld * 2) + (uint32_t)(d.row0 + km_chunk(k) * 8) * 2;
+      }
+      rstep = (uint32_t)BK * ld * 2;
+    }
+    if constexpr (MODE == G1DW) isrc = make_rsrc(p.row_src, (uint32_t)(p.S * 4));
+  };
+
+  // G1DW: the x row offsets of stage s (one per column block of this lane).
+  auto fetch_tok = [&](int s, uint32_t (&tk)[NTOK > 0 ? NTOK : 1]) {
+    if constexpr (MODE == G1DW) {
+#pragma unroll
+      for (int i = 0; i < NTOK; ++i) {
+        const int kr = s * BK + km_krow(wid + 4 * i);
+        const int idx = __builtin_amdgcn_raw_buffer_load_b32(
+            isrc, (uint32_t)(kb_cur + kr) * 4, 0, 0);
+        tk[i] = (kr < ke_cur - kb_cur) ? (uint32_t)(idx / p.topk) * (uint32_t)(H * 2) : kOOB;
+      }
     }
   };
 
-  // One register set holds one k-stage in flight: row operand + column operand.
-  struct Regs {
-    u32x4 r[TOKEN ? RPASS : 8];
-    u32x4 c[8];
-  };
-  // G1DW gathers hidden_states rows through row_src; the byte offsets of the
-  // next stage's rows are fetched one load ahead so that no load waits on a
-  // dependent index load.
-  uint32_t tokoff[8];
-  auto fetch_tok = [&](const Src& s, int kt) {
-    if constexpr (MODE == G1DW) {
-      const int f0 = s.ct * BC + fb * 8;
+  // Issues the DMA of stage s into LDS buffer s % NSTAGE.
+  auto issue_stage = [&](int s, const uint32_t (&tk)[NTOK > 0 ? NTOK : 1]) {
+    char* base = (char*)smem + (s & (NSTAGE - 1)) * STAGE_B;
 #pragma unroll
-      for (int r = 0; r < 8; ++r) {
-        const int kr = kt * BK + kb * 8 + r;
-        uint32_t off = kOOB;
-        if (kr < s.kend - s.kbeg && f0 < H)
-          off = (uint32_t)(p.row_src[s.kbeg + kr] / p.topk) * (uint32_t)(H * 2) + (uint32_t)f0 * 2;
-        tokoff[r] = off;
+    for (int i = 0; i < CBLK / 4; ++i) {
+      uint32_t off;
+      if constexpr (MODE == G1DW) off = tk[i] == kOOB ? kOOB : tk[i] + coff[i];
+      else off = coff[i] + (uint32_t)s * cstep;
+      dma16(csrc, off, base + (wid + 4 * i) * 1024);
+    }
+#pragma unroll
+    for (int i = 0; i < RPW; ++i)
+      dma16(rsrc, roff[i] + (uint32_t)s * rstep, base + CREG + (wid + 4 * i) * 1024);
+  };
+
+  // Fragment reads from stage buffer sb, sub-step ks (16 k).
+  auto read_frags = [&](int sb, int ks, bf16x8 (&af)[TI], bf16x8 (&bfr)[TJ]) {
+    const bf16* sC = smem + sb * (STAGE_B / 2);
+    const bf16* sR = sC + CREG / 2;
+    if constexpr (!COL_KM) {
+#pragma unroll
+      for (int i = 0; i < TI; ++i) {
+        const int f = wc * 128 + i * 32 + l32;
+        const int c = (2 * ks + hl) ^ ((f >> 2) & 3);
+        af[i] = *(const bf16x8*)(sC + f * BK + c * 8);
+      }
+    } else {
+      const int g = lane >> 4, j = lane & 15;
+      const int k0 = ks * 16 + 8 * (g >> 1) + (j >> 2);
+#pragma unroll
+      for (int i = 0; i < TI; ++i) {
+        const int n = wc * 128 + i * 32 + 16 * (g & 1) + 4 * (j & 3);
+        const int ka = k0, kb = k0 + 4;
+        const bf16* pa = sC + ka * BC + (((n >> 3) ^ ((ka & 3) << 2)) << 3) + (n & 4);
+        const bf16* pb = sC + kb * BC + (((n >> 3) ^ ((kb & 3) << 2)) << 3) + (n & 4);
+        af[i] = tr_frag(pa, pb);
       }
     }
-  };
-  auto load_tiles = [&](const Src& s, int kt, Regs& R) {
-    const uint32_t kbytes = (uint32_t)kt * BK * 2;
-    if constexpr (TOKEN) {
+    if constexpr (!ROW_KM) {
 #pragma unroll
-      for (int q = 0; q < RPASS; ++q) R.r[q] = bload(s.r, s.roff[q] + kbytes);
+      for (int j = 0; j < TJ; ++j) {
+        const int f = wr * WR + j * 32 + l32;
+        const int c = (2 * ks + hl) ^ ((f >> 2) & 3);
+        bfr[j] = *(const bf16x8*)(sR + f * BK + c * 8);
+      }
     } else {
-      const uint32_t base = s.roff[0] + (uint32_t)kt * BK * s.rstride;
+      const int g = lane >> 4, jj = lane & 15;
+      const int k0 = ks * 16 + 8 * (g >> 1) + (jj >> 2);
 #pragma unroll
-      for (int r = 0; r < 8; ++r) R.r[r] = bload(s.r, base + r * s.rstride);
-    }
-    if constexpr (!COL_T) {
-#pragma unroll
-      for (int q = 0; q < 8; ++q) R.c[q] = bload(s.c, s.coff[q] + kbytes);
-    } else if constexpr (MODE == G1DW) {
-#pragma unroll
-      for (int r = 0; r < 8; ++r) R.c[r] = bload(s.c, tokoff[r]);
-      fetch_tok(s, kt + 1);
-    } else {
-      const uint32_t base = s.coff[0] + (uint32_t)kt * BK * s.cstride;
-#pragma unroll
-      for (int r = 0; r < 8; ++r) R.c[r] = bload(s.c, base + r * s.cstride);
-    }
-  };
-  auto store_tiles = [&](int stage, const Regs& R) {
-    bf16* sC = smem + stage * STAGE;
-    bf16* sR = sC + BC * BK;
-    if constexpr (!COL_T) {
-#pragma unroll
-      for (int q = 0; q < 8; ++q)
-        *(u32x4*)(sC + (drow + 32 * q) * BK + dswz) = R.c[q];
-    } else {
-      store_transposed(sC, R.c, fb, kb);
-    }
-    if constexpr (TOKEN) {
-#pragma unroll
-      for (int q = 0; q < RPASS; ++q)
-        *(u32x4*)(sR + (drow + 32 * q) * BK + dswz) = R.r[q];
-    } else {
-      store_transposed(sR, R.r, fb, kb);
+      for (int j = 0; j < TJ; ++j) {
+        const int n = wr * WR + j * 32 + 16 * (g & 1) + 4 * (jj & 3);
+        const int ka = k0, kb = k0 + 4;
+        const bf16* pa = sR + ka * BR + (((n >> 3) ^ ((ka & 3) << 2)) << 3) + (n & 4);
+        const bf16* pb = sR + kb * BR + (((n >> 3) ^ ((kb & 3) << 2)) << 3) + (n & 4);
+        bfr[j] = tr_frag(pa, pb);
+      }
     }
   };
 
   f32x16 acc[TI][TJ];
-  const int fr_sw = (l32 >> 1) & 7;
-  auto read_frags = [&](int stage, int ks, bf16x8 (&af)[TI], bf16x8 (&bfr)[TJ]) {
-    const bf16* sC = smem + stage * STAGE;
-    const bf16* sR = sC + BC * BK;
-    const int csw = ((2 * ks + hl) ^ fr_sw) << 3;
-#pragma unroll
-    for (int i = 0; i < TI; ++i)
-      af[i] = *(const bf16x8*)(sC + (wc * 128 + i * 32 + l32) * BK + csw);
-#pragma unroll
-    for (int j = 0; j < TJ; ++j)
-      bfr[j] = *(const bf16x8*)(sR + (wr * WR + j * 32 + l32) * BK + csw);
-  };
   auto mfmas = [&](const bf16x8 (&af)[TI], const bf16x8 (&bfr)[TJ]) {
 #pragma unroll
     for (int i = 0; i < TI; ++i)
@@ -339,14 +369,9 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
   };
 
-  Tile cur = decode(t);
-  Src src;
-  setup(cur, src);
-  Regs R;
-  fetch_tok(src, 0);
-  load_tiles(src, 0, R);
-
-  while (true) {
+  for (; t < t_end; t += nslot) {
+    const Tile cur = decode(t);
+    setup(cur);
 #pragma unroll
     for (int i = 0; i < TI; ++i)
 #pragma unroll
@@ -354,47 +379,48 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-    // ------------------------------------------------------- main loop
-    // LDS holds two k-stages; the global loads for stage kt+1 are issued at
-    // the top of step kt, land in registers while the MFMAs of step kt run
-    // and are written to the other stage before the step's single barrier.
-    // The last step is peeled so the loop body is one basic block.
+    // --------------------------------------------------------- main loop
+    // Every step issues PER vector-memory ops (the DMA of stage kt+3, plus
+    // for G1DW the row indices of stage kt+5), so before consuming stage kt
+    // exactly 2*PER younger ops may still be outstanding.  Stages past the
+    // last one are still issued (their loads read zeros or in-bounds bytes
+    // that are never used) to keep that count exact.
     if (cur.nk > 0) {
-      auto kstep = [&](int kt, bool has_next) {
-        const int stg = kt & 1;
-        if (has_next) load_tiles(src, kt + 1, R);
-        // Keep the loads at the top of the step: the scheduler would
-        // otherwise sink them next to their LDS stores.
-        __builtin_amdgcn_sched_barrier(0);
+      fetch_tok(0, tokA);
+      fetch_tok(1, tokB);
 #pragma unroll
-        for (int ks = 0; ks < BK / 16; ++ks) {
-          bf16x8 af[TI], bfr[TJ];
-          read_frags(stg, ks, af, bfr);
-          mfmas(af, bfr);
+      for (int s = 0; s < NSTAGE - 1; ++s) {
+        uint32_t tn[NTOK > 0 ? NTOK : 1];
+        fetch_tok(s + 2, tn);
+        issue_stage(s, tokA);
+        if constexpr (NTOK > 0) {
+#pragma unroll
+          for (int i = 0; i < NTOK; ++i) { tokA[i] = tokB[i]; tokB[i] = tn[i]; }
         }
-        if (has_next) {
-          store_tiles(stg ^ 1, R);
-          __syncthreads();
+      }
+      for (int kt = 0; kt < cur.nk; ++kt) {
+        WAIT_VMCNT(2 * PER);
+        __builtin_amdgcn_s_barrier();  // stage kt visible; buffer of stage kt-1 free
+        {
+          uint32_t tn[NTOK > 0 ? NTOK : 1];
+          fetch_tok(kt + NSTAGE + 1, tn);
+          issue_stage(kt + NSTAGE - 1, tokA);
+          if constexpr (NTOK > 0) {
+#pragma unroll
+            for (int i = 0; i < NTOK; ++i) { tokA[i] = tokB[i]; tokB[i] = tn[i]; }
+          }
         }
-      };
-      store_tiles(0, R);
-      __syncthreads();
-      for (int kt = 0; kt < cur.nk - 1; ++kt) kstep(kt, true);
-      kstep(cur.nk - 1, false);
-    }
-
-    // --------------------------------------- next tile's first stage load
-    const int tn = t + nslot;
-    const bool more = tn < t_end;
-    Tile nxt = cur;
-    if (more) {
-      nxt = decode(tn);
-      setup(nxt, src);
-      fetch_tok(src, 0);
-      load_tiles(src, 0, R);
+        const int sb = kt & (NSTAGE - 1);
+        bf16x8 a0[TI], b0[TJ], a1[TI], b1[TJ];
+        read_frags(sb, 0, a0, b0);
+        read_frags(sb, 1, a1, b1);
+        mfmas(a0, b0);
+        mfmas(a1, b1);
+      }
     }
 
     // --------------------------------------------------------- epilogue
+    WAIT_VMCNT(0);    // no LDS DMA may still be landing in the stages
     __syncthreads();  // every wave is done reading the k-stages
     bf16* stg = smem;  // [BR][SROW] bf16 staging tile
 #pragma unroll
@@ -490,10 +516,7 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
           *(u32x4*)(obase + (int64_t)r * ld + f) = *(const u32x4*)(stg + row * SROW + c0);
       }
     }
-    if (!more) break;
-    __syncthreads();  // staging reads done before stage 0 is overwritten
-    t = tn;
-    cur = nxt;
+    __syncthreads();  // staging reads done before the next tile's stages land
   }
 }
 
@@ -513,7 +536,7 @@ int num_cus() {
 
 template <int MODE, int BR>
 int launch(const GemmArgs& a, int max_tiles, hipStream_t st) {
-  constexpr size_t stages = (size_t)2 * (BC + BR) * BK * sizeof(bf16);
+  constexpr size_t stages = (size_t)NSTAGE * (BC + BR) * BK * sizeof(bf16);
   constexpr size_t staging = (size_t)BR * SROW * sizeof(bf16);
   const size_t lds = stages > staging ? stages : staging;
   if (max_tiles <= 0) return MOE_OK;
