@@ -74,6 +74,8 @@ struct GemmArgs {
   bf16* out2;            // gate_up output of G1F (may be null)
   int64_t T, S;
   int E, H, I, topk;
+  uint32_t tok_mul;      // n / topk == (n * tok_mul) >> tok_shift for 0 <= n < 2^31
+  int tok_shift;         // 31 + ceil(log2(topk))
   int n_ct, n_rt, n_tiles;  // n_tiles: dW modes (host-known)
 };
 
@@ -98,13 +100,30 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, v
 constexpr int vmcnt_imm(int n) { return (n & 15) | (7 << 4) | (15 << 8) | (((n >> 4) & 3) << 14); }
 #define WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(vmcnt_imm(n))
 
+// One transpose read.  The restrict-qualified parameter gives the load an
+// alias scope once inlined, which tells the compiler's wait-count insertion
+// that it does not alias the in-flight LDS DMA; without it a full
+// vmcnt(0) drain is placed before every such read.  Ordering against the DMA
+// is explicit in the main loop (s_waitcnt vmcnt + s_barrier).
+__device__ __forceinline__ s16x4 read_tr(const lds_s16x4_t* __restrict__ p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<lds_s16x4_t*>(p));
+}
+
 // One MFMA fragment (8 consecutive k of one feature) from a k-major stage
 // region: two transpose reads, k 0..3 and k 4..7.
 __device__ __forceinline__ bf16x8 tr_frag(const bf16* p0, const bf16* p1) {
-  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)p0);
-  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)p1);
+  const s16x4 lo = read_tr((const lds_s16x4_t*)p0);
+  const s16x4 hi = read_tr((const lds_s16x4_t*)p1);
   const s16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
   return __builtin_bit_cast(bf16x8, v);
+}
+
+// Token of a routed row: row_src / topk by multiply-shift (Granlund and
+// Montgomery, "Division by invariant integers using multiplication", 1994):
+// with s = ceil(log2 d) and m = ceil(2^(31+s) / d), m < 2^32 and
+// floor(n*m / 2^(31+s)) == floor(n / d) for every 0 <= n < 2^31.
+__device__ __forceinline__ int div_topk(int n, uint32_t m, int shift) {
+  return (int)(((uint64_t)(uint32_t)n * m) >> shift);
 }
 
 template <int MODE, int BR>
@@ -197,8 +216,8 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
   uint32_t coff[CBLK / 4];   // byte offsets of this lane's column blocks at stage 0
   uint32_t roff[RPW > 0 ? RPW : 1];
   uint32_t cstep = 0, rstep = 0;  // byte advance per stage
-  // G1DW: byte offsets of the gathered x rows, rotated through three stages.
-  uint32_t tokA[NTOK > 0 ? NTOK : 1], tokB[NTOK > 0 ? NTOK : 1];
+  // G1DW: row_src entries of the three stages ahead of the next DMA.
+  int tokA[NTOK > 0 ? NTOK : 1], tokB[NTOK > 0 ? NTOK : 1], tokC[NTOK > 0 ? NTOK : 1];
   int ctile = 0, cfeat0 = 0, kb_cur = 0, ke_cur = 0;
 
   auto setup = [&](const Tile& d) {
@@ -259,7 +278,7 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
       for (int i = 0; i < RPW; ++i) {
         const int f = kc_feature(wid + 4 * i);  // row-region block index wid + 4*i
         const int r = min(d.row0 + f, d.row_end - 1);
-        const int tok = p.row_src[r] / p.topk;
+        const int tok = div_topk(p.row_src[r], p.tok_mul, p.tok_shift);
         roff[i] = (uint32_t)tok * (uint32_t)(H * 2) + kc_chunk(f) * 16;
       }
       rstep = BK * 2;
@@ -288,27 +307,32 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
     if constexpr (MODE == G1DW) isrc = make_rsrc(p.row_src, (uint32_t)(p.S * 4));
   };
 
-  // G1DW: the x row offsets of stage s (one per column block of this lane).
-  auto fetch_tok = [&](int s, uint32_t (&tk)[NTOK > 0 ? NTOK : 1]) {
+  // G1DW: raw row_src entries of stage s (one per column block of this
+  // lane), loaded three stages ahead.  Reads past S return zero; rows past
+  // the expert's range are masked when the DMA offsets are formed.
+  auto fetch_tok = [&](int s, int (&tk)[NTOK > 0 ? NTOK : 1]) {
     if constexpr (MODE == G1DW) {
 #pragma unroll
       for (int i = 0; i < NTOK; ++i) {
         const int kr = s * BK + km_krow(wid + 4 * i);
-        const int idx = __builtin_amdgcn_raw_buffer_load_b32(
-            isrc, (uint32_t)(kb_cur + kr) * 4, 0, 0);
-        tk[i] = (kr < ke_cur - kb_cur) ? (uint32_t)(idx / p.topk) * (uint32_t)(H * 2) : kOOB;
+        tk[i] = __builtin_amdgcn_raw_buffer_load_b32(isrc, (uint32_t)(kb_cur + kr) * 4, 0, 0);
       }
     }
   };
 
   // Issues the DMA of stage s into LDS buffer s % NSTAGE.
-  auto issue_stage = [&](int s, const uint32_t (&tk)[NTOK > 0 ? NTOK : 1]) {
+  auto issue_stage = [&](int s, const int (&tk)[NTOK > 0 ? NTOK : 1]) {
     char* base = (char*)smem + (s & (NSTAGE - 1)) * STAGE_B;
 #pragma unroll
     for (int i = 0; i < CBLK / 4; ++i) {
       uint32_t off;
-      if constexpr (MODE == G1DW) off = tk[i] == kOOB ? kOOB : tk[i] + coff[i];
-      else off = coff[i] + (uint32_t)s * cstep;
+      if constexpr (MODE == G1DW) {
+        const int kr = s * BK + km_krow(wid + 4 * i);
+        off = kr < ke_cur - kb_cur ? (uint32_t)div_topk(tk[i], p.tok_mul, p.tok_shift) * (uint32_t)(H * 2) + coff[i]
+                                   : kOOB;
+      } else {
+        off = coff[i] + (uint32_t)s * cstep;
+      }
       dma16(csrc, off, base + (wid + 4 * i) * 1024);
     }
 #pragma unroll
@@ -380,34 +404,36 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
     // --------------------------------------------------------- main loop
-    // Every step issues PER vector-memory ops (the DMA of stage kt+3, plus
-    // for G1DW the row indices of stage kt+5), so before consuming stage kt
-    // exactly 2*PER younger ops may still be outstanding.  Stages past the
-    // last one are still issued (their loads read zeros or in-bounds bytes
-    // that are never used) to keep that count exact.
+    // Every step issues PER vector-memory ops (the DMA of stage kt+3, then
+    // for G1DW the row_src entries of stage kt+6), so before consuming stage
+    // kt exactly 2*PER younger ops may still be outstanding; that wait also
+    // covers the row_src entries of stage kt+3 used by this step's DMA.
+    // Stages past the last one are still issued (their loads read zeros or
+    // in-bounds bytes that are never used) to keep that count exact.
     if (cur.nk > 0) {
       fetch_tok(0, tokA);
       fetch_tok(1, tokB);
+      fetch_tok(2, tokC);
 #pragma unroll
       for (int s = 0; s < NSTAGE - 1; ++s) {
-        uint32_t tn[NTOK > 0 ? NTOK : 1];
-        fetch_tok(s + 2, tn);
         issue_stage(s, tokA);
+        int tn[NTOK > 0 ? NTOK : 1];
+        fetch_tok(s + 3, tn);
         if constexpr (NTOK > 0) {
 #pragma unroll
-          for (int i = 0; i < NTOK; ++i) { tokA[i] = tokB[i]; tokB[i] = tn[i]; }
+          for (int i = 0; i < NTOK; ++i) { tokA[i] = tokB[i]; tokB[i] = tokC[i]; tokC[i] = tn[i]; }
         }
       }
       for (int kt = 0; kt < cur.nk; ++kt) {
         WAIT_VMCNT(2 * PER);
         __builtin_amdgcn_s_barrier();  // stage kt visible; buffer of stage kt-1 free
         {
-          uint32_t tn[NTOK > 0 ? NTOK : 1];
-          fetch_tok(kt + NSTAGE + 1, tn);
           issue_stage(kt + NSTAGE - 1, tokA);
+          int tn[NTOK > 0 ? NTOK : 1];
+          fetch_tok(kt + NSTAGE - 1 + 3, tn);
           if constexpr (NTOK > 0) {
 #pragma unroll
-            for (int i = 0; i < NTOK; ++i) { tokA[i] = tokB[i]; tokB[i] = tn[i]; }
+            for (int i = 0; i < NTOK; ++i) { tokA[i] = tokB[i]; tokB[i] = tokC[i]; tokC[i] = tn[i]; }
           }
         }
         const int sb = kt & (NSTAGE - 1);
@@ -518,6 +544,14 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
     }
     __syncthreads();  // staging reads done before the next tile's stages land
   }
+}
+
+void set_topk(GemmArgs& a, int top_k) {
+  a.topk = top_k;
+  int sh = 0;
+  while ((1 << sh) < top_k) ++sh;
+  a.tok_shift = 31 + sh;
+  a.tok_mul = (uint32_t)((((uint64_t)1 << (31 + sh)) + (uint64_t)top_k - 1) / (uint64_t)top_k);
 }
 
 int g_num_cu[64];
@@ -634,7 +668,7 @@ extern "C" int moe_amd_gemm_gate_up_swiglu(const void* hidden_states, const int3
   a.offsets = offsets;
   a.out = (bf16*)act_out;
   a.out2 = (bf16*)gate_up_out;
-  a.T = T; a.S = S; a.E = E; a.H = H; a.I = I; a.topk = top_k;
+  a.T = T; a.S = S; a.E = E; a.H = H; a.I = I; set_topk(a, top_k);
   return launch_token<G1F>(a, S, E, 128, I, tile_plan, (hipStream_t)stream);
 }
 
@@ -756,7 +790,7 @@ extern "C" int moe_amd_gemm_gate_up_backward_dw(const void* d_gate_up, const voi
   a.row_src = row_src;
   a.offsets = offsets;
   a.out = (bf16*)d_gate_up_proj;
-  a.T = T; a.S = S; a.E = E; a.H = H; a.I = I; a.topk = top_k;
+  a.T = T; a.S = S; a.E = E; a.H = H; a.I = I; set_topk(a, top_k);
   a.n_rt = (2 * I + 255) / 256;
   a.n_ct = (H + BC - 1) / BC;
   a.n_tiles = E * a.n_rt * a.n_ct;
