@@ -16,14 +16,18 @@
 //
 // Data path: global -> LDS by DMA (gfx950 `buffer_load_dwordx4 ... lds`: lane
 // L of a wave instruction writes 16 bytes at M0 + 16*L), so operands cost no
-// VGPRs and no ds_write.  LDS holds 4 stages of BK = 32; while stage kt is
-// consumed, stages kt+1..kt+3 are in flight, each wave counting its own DMA
+// VGPRs and no ds_write.  A k-stage is BK = 64 deep, so every row of a
+// k-contiguous operand is fetched as one full 128-byte line (64-byte row
+// pieces halve a CU's achievable load rate).  LDS is a ring of five 32 KB
+// slots, each holding one operand's half of a stage (column half: 256
+// features x 64 k; row half: BR rows x 64 k); while stage kt is consumed the
+// three following half-stages are in flight, each wave counting its own DMA
 // with s_waitcnt vmcnt before the stage barrier.  Two LDS layouts:
 //   * k-contiguous operands (activation rows, the forward weights) are kept
-//     as [feature][32 k] (64-byte rows, 16-byte chunks XOR-swizzled by
-//     (feature >> 2) & 3) and read with ds_read_b128;
+//     as [feature][64 k] (128-byte rows, 16-byte chunks XOR-swizzled by
+//     (feature >> 1) & 7) and read with ds_read_b128;
 //   * k-major operands (the weights of the dX GEMMs, every operand of the dW
-//     GEMMs) are copied as they lie, [32 k][features] (16-byte chunks
+//     GEMMs) are copied as they lie, [64 k][features] (16-byte chunks
 //     swizzled by (k & 3) << 2), and read with ds_read_b64_tr_b16, whose
 //     16-lane transpose turns four 8-byte row reads into one lane's four
 //     consecutive k values -- no register transposes.
@@ -53,8 +57,9 @@
 namespace moe {
 namespace {
 
-constexpr int BK = 32;     // k per LDS stage
-constexpr int NSTAGE = 4;  // LDS stages: one consumed, three in flight
+constexpr int BK = 64;       // k per stage
+constexpr int SLOT = 32768;  // bytes per LDS slot (one operand's half of a stage)
+constexpr int NSLOT = 5;     // ring of half-stages: two consumed, three in flight
 constexpr int BC = 256;    // output columns per workgroup
 constexpr int NTHR = 256;  // 4 waves
 constexpr int SROW = 260;  // bf16 per row of the epilogue staging tile (520 B: conflict-free)
@@ -99,6 +104,8 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, v
 // s_waitcnt encodings (gfx9 family): vmcnt in [3:0]+[15:14], lgkmcnt [11:8].
 constexpr int vmcnt_imm(int n) { return (n & 15) | (7 << 4) | (15 << 8) | (((n >> 4) & 3) << 14); }
 #define WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(vmcnt_imm(n))
+// vmcnt(n) and lgkmcnt(0) together.
+#define WAIT_VMCNT_LGKM0(n) __builtin_amdgcn_s_waitcnt(vmcnt_imm(n) & ~(15 << 8))
 
 // One transpose read.  The restrict-qualified parameter gives the load an
 // alias scope once inlined, which tells the compiler's wait-count insertion
@@ -128,21 +135,18 @@ __device__ __forceinline__ int div_topk(int n, uint32_t m, int shift) {
 
 template <int MODE, int BR>
 __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
-  constexpr bool TOKEN = MODE <= G1DX;                  // rows = routed rows of one expert
+  constexpr bool TOKEN = MODE <= G1DX;                    // rows = routed rows of one expert
   constexpr bool COL_KM = !(MODE == G1F || MODE == G2F);  // column operand k-major in memory
-  constexpr bool ROW_KM = !TOKEN;                       // row operand k-major (dW)
-  constexpr int WR = BR / 2;                            // rows per wave
-  constexpr int TJ = WR / 32;                           // MFMA row sub-tiles per wave
-  constexpr int TI = 4;                                 // MFMA col sub-tiles per wave (128 cols)
-  constexpr int CREG = BC * BK * 2;                     // bytes of the column region per stage
-  constexpr int RREG = BR * BK * 2;                     // bytes of the row region per stage
-  constexpr int STAGE_B = CREG + RREG;
-  constexpr int CBLK = CREG / 1024, RBLK = RREG / 1024; // 1 KB DMA blocks per region
-  constexpr int BPW = (CBLK + RBLK) / 4;                // DMA blocks per wave per stage
-  constexpr int RPW = BPW - CBLK / 4;                   // ... of which in the row region
-  constexpr int NTOK = (MODE == G1DW) ? CBLK / 4 : 0;   // gathered-row index loads per stage
-  constexpr int PER = BPW + NTOK;                       // vector-memory ops per stage issue
-  static_assert((CBLK + RBLK) % 4 == 0 && CBLK % 4 == 0, "DMA blocks per wave");
+  constexpr bool ROW_KM = !TOKEN;                         // row operand k-major (dW)
+  constexpr int WR = BR / 2;                              // rows per wave
+  constexpr int TJ = WR / 32;                             // MFMA row sub-tiles per wave
+  constexpr int TI = 4;                                   // MFMA col sub-tiles per wave (128 cols)
+  constexpr int CPW = BC * BK * 2 / 1024 / 4;             // 1 KB DMA blocks per wave, column half
+  constexpr int RPW = BR * BK * 2 / 1024 / 4;             // ... row half
+  constexpr int NTOK = (MODE == G1DW) ? CPW : 0;          // gathered-row indices per lane and stage
+  constexpr int NOPS = NTOK + RPW + CPW;                  // memory ops per main-loop step
+  constexpr int NGRP = (BK / 16) * TI;                    // MFMA groups per step
+  static_assert(CPW == 8 && RPW * 32 == BR, "DMA blocks per wave");
   static_assert(TOKEN || BR == 256, "dW modes use 256-row tiles");
 
   extern __shared__ __attribute__((aligned(16))) bf16 smem[];
@@ -201,34 +205,30 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
   };
 
   // ------------------------------------------------------- DMA geometry
-  // Wave w fills the 1 KB blocks w, w+4, w+8, ... of each stage: blocks
-  // 0..CBLK-1 hold the column operand, the rest the row operand.  Within a
-  // block of a k-contiguous region, lane L carries feature 16*blk + L/4 and
-  // physical chunk L&3 (logical chunk (L&3) ^ ((feature>>2)&3)); within a
-  // block of a k-major region it carries k row 2*blk + L/32 and physical
-  // chunk L&31 (logical chunk (L&31) ^ ((k&3)<<2), 8 features per chunk).
-  auto kc_feature = [&](int blk) { return blk * 16 + (lane >> 2); };
-  auto kc_chunk = [&](int f) { return (lane & 3) ^ ((f >> 2) & 3); };
+  // Wave w fills the 1 KB blocks w, w+4, w+8, ... of each half-stage.  In a
+  // k-contiguous half, lane L carries feature 8*blk + L/8 and physical chunk
+  // L&7, which holds logical chunk (L&7) ^ ((feature>>1)&7).  In a k-major
+  // half it carries k row 2*blk + L/32 and physical chunk L&31, which holds
+  // logical chunk (L&31) ^ ((k&3)<<2) (8 features per chunk).
+  auto kc_feature = [&](int blk) { return blk * 8 + (lane >> 3); };
+  auto kc_chunk = [&](int f) { return (lane & 7) ^ ((f >> 1) & 7); };
   auto km_krow = [&](int blk) { return blk * 2 + (lane >> 5); };
   auto km_chunk = [&](int k) { return (lane & 31) ^ ((k & 3) << 2); };
 
   __amdgpu_buffer_rsrc_t csrc, rsrc, isrc;
-  uint32_t coff[CBLK / 4];   // byte offsets of this lane's column blocks at stage 0
-  uint32_t roff[RPW > 0 ? RPW : 1];
+  uint32_t coff[CPW];  // byte offsets of this lane's column blocks at stage 0
+  uint32_t roff[RPW];
   uint32_t cstep = 0, rstep = 0;  // byte advance per stage
-  // G1DW: row_src entries of the three stages ahead of the next DMA.
-  int tokA[NTOK > 0 ? NTOK : 1], tokB[NTOK > 0 ? NTOK : 1], tokC[NTOK > 0 ? NTOK : 1];
-  int ctile = 0, cfeat0 = 0, kb_cur = 0, ke_cur = 0;
+  int kb_cur = 0, ke_cur = 0;
 
   auto setup = [&](const Tile& d) {
-    ctile = d.ct;
     kb_cur = d.kbeg;
     ke_cur = d.kend;
     // Column operand.
     if constexpr (MODE == G1F) {
       csrc = make_rsrc(p.w + (int64_t)d.e * I2 * H, (uint32_t)(I2 * H * 2));
 #pragma unroll
-      for (int i = 0; i < CBLK / 4; ++i) {
+      for (int i = 0; i < CPW; ++i) {
         const int f = kc_feature(wid + 4 * i);  // tile column: [gate 64 | up 64] per wave column
         const int lc = f & 127;
         const int feat = d.ct * 128 + (f >> 7) * 64 + (lc & 63);
@@ -239,7 +239,7 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
     } else if constexpr (MODE == G2F) {
       csrc = make_rsrc(p.w + (int64_t)d.e * H * I, (uint32_t)(H * I * 2));
 #pragma unroll
-      for (int i = 0; i < CBLK / 4; ++i) {
+      for (int i = 0; i < CPW; ++i) {
         const int f = kc_feature(wid + 4 * i);
         const int wrow = d.ct * BC + f;
         coff[i] = wrow < H ? (uint32_t)wrow * (uint32_t)(I * 2) + kc_chunk(f) * 16 : kOOB;
@@ -262,11 +262,10 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
         csrc = make_rsrc(p.x, (uint32_t)(p.T * H * 2));
         ld = H;
       }
-      cfeat0 = d.ct * BC;
 #pragma unroll
-      for (int i = 0; i < CBLK / 4; ++i) {
+      for (int i = 0; i < CPW; ++i) {
         const int k = km_krow(wid + 4 * i);
-        const uint32_t fb = (uint32_t)(cfeat0 + km_chunk(k) * 8) * 2;
+        const uint32_t fb = (uint32_t)(d.ct * BC + km_chunk(k) * 8) * 2;
         coff[i] = (MODE == G1DW) ? fb : (uint32_t)k * (uint32_t)(ld * 2) + fb;
       }
       cstep = (MODE == G1DW) ? 0 : (uint32_t)BK * ld * 2;
@@ -276,7 +275,7 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
       rsrc = make_rsrc(p.x, (uint32_t)(p.T * H * 2));
 #pragma unroll
       for (int i = 0; i < RPW; ++i) {
-        const int f = kc_feature(wid + 4 * i);  // row-region block index wid + 4*i
+        const int f = kc_feature(wid + 4 * i);
         const int r = min(d.row0 + f, d.row_end - 1);
         const int tok = div_topk(p.row_src[r], p.tok_mul, p.tok_shift);
         roff[i] = (uint32_t)tok * (uint32_t)(H * 2) + kc_chunk(f) * 16;
@@ -308,8 +307,8 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
   };
 
   // G1DW: raw row_src entries of stage s (one per column block of this
-  // lane), loaded three stages ahead.  Reads past S return zero; rows past
-  // the expert's range are masked when the DMA offsets are formed.
+  // lane).  Reads past S return zero; rows past the expert's range are
+  // masked when the DMA offsets are formed.
   auto fetch_tok = [&](int s, int (&tk)[NTOK > 0 ? NTOK : 1]) {
     if constexpr (MODE == G1DW) {
 #pragma unroll
@@ -320,78 +319,65 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
     }
   };
 
-  // Issues the DMA of stage s into LDS buffer s % NSTAGE.
-  auto issue_stage = [&](int s, const int (&tk)[NTOK > 0 ? NTOK : 1]) {
-    char* base = (char*)smem + (s & (NSTAGE - 1)) * STAGE_B;
+  auto slot_ptr = [&](int h) { return (char*)smem + (h % NSLOT) * SLOT; };
+
+  // DMA of the column half of stage s (ring position 2s).
+  auto issue_col = [&](int s, const int (&tk)[NTOK > 0 ? NTOK : 1]) {
+    char* base = slot_ptr(2 * s);
 #pragma unroll
-    for (int i = 0; i < CBLK / 4; ++i) {
+    for (int i = 0; i < CPW; ++i) {
       uint32_t off;
       if constexpr (MODE == G1DW) {
         const int kr = s * BK + km_krow(wid + 4 * i);
-        off = kr < ke_cur - kb_cur ? (uint32_t)div_topk(tk[i], p.tok_mul, p.tok_shift) * (uint32_t)(H * 2) + coff[i]
-                                   : kOOB;
+        off = kr < ke_cur - kb_cur
+                  ? (uint32_t)div_topk(tk[i], p.tok_mul, p.tok_shift) * (uint32_t)(H * 2) + coff[i]
+                  : kOOB;
       } else {
         off = coff[i] + (uint32_t)s * cstep;
       }
       dma16(csrc, off, base + (wid + 4 * i) * 1024);
     }
+  };
+  // DMA of the row half of stage s (ring position 2s+1).
+  auto issue_row = [&](int s) {
+    char* base = slot_ptr(2 * s + 1);
 #pragma unroll
     for (int i = 0; i < RPW; ++i)
-      dma16(rsrc, roff[i] + (uint32_t)s * rstep, base + CREG + (wid + 4 * i) * 1024);
+      dma16(rsrc, roff[i] + (uint32_t)s * rstep, base + (wid + 4 * i) * 1024);
   };
 
-  // Fragment reads from stage buffer sb, sub-step ks (16 k).
-  auto read_frags = [&](int sb, int ks, bf16x8 (&af)[TI], bf16x8 (&bfr)[TJ]) {
-    const bf16* sC = smem + sb * (STAGE_B / 2);
-    const bf16* sR = sC + CREG / 2;
+  // Fragment reads of k sub-step ks (16 k) from the column / row slots:
+  // column sub-tile i, row sub-tile j.
+  auto read_a = [&](const bf16* sC, int ks, int i) -> bf16x8 {
     if constexpr (!COL_KM) {
-#pragma unroll
-      for (int i = 0; i < TI; ++i) {
-        const int f = wc * 128 + i * 32 + l32;
-        const int c = (2 * ks + hl) ^ ((f >> 2) & 3);
-        af[i] = *(const bf16x8*)(sC + f * BK + c * 8);
-      }
-    } else {
-      const int g = lane >> 4, j = lane & 15;
-      const int k0 = ks * 16 + 8 * (g >> 1) + (j >> 2);
-#pragma unroll
-      for (int i = 0; i < TI; ++i) {
-        const int n = wc * 128 + i * 32 + 16 * (g & 1) + 4 * (j & 3);
-        const int ka = k0, kb = k0 + 4;
-        const bf16* pa = sC + ka * BC + (((n >> 3) ^ ((ka & 3) << 2)) << 3) + (n & 4);
-        const bf16* pb = sC + kb * BC + (((n >> 3) ^ ((kb & 3) << 2)) << 3) + (n & 4);
-        af[i] = tr_frag(pa, pb);
-      }
-    }
-    if constexpr (!ROW_KM) {
-#pragma unroll
-      for (int j = 0; j < TJ; ++j) {
-        const int f = wr * WR + j * 32 + l32;
-        const int c = (2 * ks + hl) ^ ((f >> 2) & 3);
-        bfr[j] = *(const bf16x8*)(sR + f * BK + c * 8);
-      }
+      const int f = wc * 128 + i * 32 + l32;
+      const int c = (2 * ks + hl) ^ ((f >> 1) & 7);
+      return *(const bf16x8*)(sC + f * BK + c * 8);
     } else {
       const int g = lane >> 4, jj = lane & 15;
-      const int k0 = ks * 16 + 8 * (g >> 1) + (jj >> 2);
-#pragma unroll
-      for (int j = 0; j < TJ; ++j) {
-        const int n = wr * WR + j * 32 + 16 * (g & 1) + 4 * (jj & 3);
-        const int ka = k0, kb = k0 + 4;
-        const bf16* pa = sR + ka * BR + (((n >> 3) ^ ((ka & 3) << 2)) << 3) + (n & 4);
-        const bf16* pb = sR + kb * BR + (((n >> 3) ^ ((kb & 3) << 2)) << 3) + (n & 4);
-        bfr[j] = tr_frag(pa, pb);
-      }
+      const int ka = ks * 16 + 8 * (g >> 1) + (jj >> 2), kb = ka + 4;  // transpose-read k rows
+      const int n = wc * 128 + i * 32 + 16 * (g & 1) + 4 * (jj & 3);
+      const bf16* pa = sC + ka * BC + (((n >> 3) ^ ((ka & 3) << 2)) << 3) + (n & 4);
+      const bf16* pb = sC + kb * BC + (((n >> 3) ^ ((kb & 3) << 2)) << 3) + (n & 4);
+      return tr_frag(pa, pb);
+    }
+  };
+  auto read_b = [&](const bf16* sR, int ks, int j) -> bf16x8 {
+    if constexpr (!ROW_KM) {
+      const int f = wr * WR + j * 32 + l32;
+      const int c = (2 * ks + hl) ^ ((f >> 1) & 7);
+      return *(const bf16x8*)(sR + f * BK + c * 8);
+    } else {
+      const int g = lane >> 4, jj = lane & 15;
+      const int ka = ks * 16 + 8 * (g >> 1) + (jj >> 2), kb = ka + 4;
+      const int n = wr * WR + j * 32 + 16 * (g & 1) + 4 * (jj & 3);
+      const bf16* pa = sR + ka * BR + (((n >> 3) ^ ((ka & 3) << 2)) << 3) + (n & 4);
+      const bf16* pb = sR + kb * BR + (((n >> 3) ^ ((kb & 3) << 2)) << 3) + (n & 4);
+      return tr_frag(pa, pb);
     }
   };
 
   f32x16 acc[TI][TJ];
-  auto mfmas = [&](const bf16x8 (&af)[TI], const bf16x8 (&bfr)[TJ]) {
-#pragma unroll
-    for (int i = 0; i < TI; ++i)
-#pragma unroll
-      for (int j = 0; j < TJ; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
-  };
 
   for (; t < t_end; t += nslot) {
     const Tile cur = decode(t);
@@ -404,44 +390,88 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
     // --------------------------------------------------------- main loop
-    // Every step issues PER vector-memory ops (the DMA of stage kt+3, then
-    // for G1DW the row_src entries of stage kt+6), so before consuming stage
-    // kt exactly 2*PER younger ops may still be outstanding; that wait also
-    // covers the row_src entries of stage kt+3 used by this step's DMA.
-    // Stages past the last one are still issued (their loads read zeros or
-    // in-bounds bytes that are never used) to keep that count exact.
+    // Ring position h holds the column half (h = 2s) or the row half
+    // (h = 2s+1) of stage s, in slot h % 5.  Step kt waits until only the
+    // last-issued column half (stage kt+1) may still be in flight, so that
+    // both halves of stage kt (and, for G1DW, the row_src entries of stage
+    // kt+2) have landed; after the barrier the slots of stage kt-1 are free
+    // and receive the row half of stage kt+1 and the column half of stage
+    // kt+2.  Stages past the last one are still issued (their loads read
+    // zeros or in-bounds bytes that are never used) to keep the count exact.
     if (cur.nk > 0) {
-      fetch_tok(0, tokA);
-      fetch_tok(1, tokB);
-      fetch_tok(2, tokC);
-#pragma unroll
-      for (int s = 0; s < NSTAGE - 1; ++s) {
-        issue_stage(s, tokA);
-        int tn[NTOK > 0 ? NTOK : 1];
-        fetch_tok(s + 3, tn);
-        if constexpr (NTOK > 0) {
-#pragma unroll
-          for (int i = 0; i < NTOK; ++i) { tokA[i] = tokB[i]; tokB[i] = tokC[i]; tokC[i] = tn[i]; }
-        }
-      }
+      int tk_a[NTOK > 0 ? NTOK : 1], tk_b[NTOK > 0 ? NTOK : 1];
+      fetch_tok(0, tk_a);
+      fetch_tok(1, tk_b);
+      issue_col(0, tk_a);
+      fetch_tok(2, tk_a);
+      issue_row(0);
+      issue_col(1, tk_b);
       for (int kt = 0; kt < cur.nk; ++kt) {
-        WAIT_VMCNT(2 * PER);
-        __builtin_amdgcn_s_barrier();  // stage kt visible; buffer of stage kt-1 free
-        {
-          issue_stage(kt + NSTAGE - 1, tokA);
-          int tn[NTOK > 0 ? NTOK : 1];
-          fetch_tok(kt + NSTAGE - 1 + 3, tn);
-          if constexpr (NTOK > 0) {
+        // lgkmcnt(0): this wave's reads of stage kt-1 are complete before
+        // the barrier lets other waves overwrite their slots.
+        WAIT_VMCNT_LGKM0(CPW);
+        __builtin_amdgcn_s_barrier();
+        const bf16* sC = (const bf16*)slot_ptr(2 * kt);
+        const bf16* sR = (const bf16*)slot_ptr(2 * kt + 1);
+        char* rdst = slot_ptr(2 * kt + 3);  // row half of stage kt+1
+        char* cdst = slot_ptr(2 * kt + 4);  // column half of stage kt+2
+        int tn[NTOK > 0 ? NTOK : 1];
+        // The step's NOPS memory ops (row_src entries of stage kt+3, DMA of
+        // the row half of kt+1, DMA of the column half of kt+2, in this
+        // order) are spread over its 16 MFMA groups: issued in one burst
+        // they back up the texture pipe and stall the wave's MFMA issue.
+        auto mem_op = [&](int o) {
+          if (o < NTOK) {
+            if constexpr (MODE == G1DW) {
+              const int kr = (kt + 3) * BK + km_krow(wid + 4 * o);
+              tn[o] = __builtin_amdgcn_raw_buffer_load_b32(isrc, (uint32_t)(kb_cur + kr) * 4, 0, 0);
+            }
+          } else if (o < NTOK + RPW) {
+            const int i = o - NTOK;
+            dma16(rsrc, roff[i] + (uint32_t)(kt + 1) * rstep, rdst + (wid + 4 * i) * 1024);
+          } else {
+            const int i = o - NTOK - RPW;
+            uint32_t off;
+            if constexpr (MODE == G1DW) {
+              const int kr = (kt + 2) * BK + km_krow(wid + 4 * i);
+              off = kr < ke_cur - kb_cur
+                        ? (uint32_t)div_topk(tk_a[i], p.tok_mul, p.tok_shift) * (uint32_t)(H * 2) + coff[i]
+                        : kOOB;
+            } else {
+              off = coff[i] + (uint32_t)(kt + 2) * cstep;
+            }
+            dma16(csrc, off, cdst + (wid + 4 * i) * 1024);
+          }
+        };
+        // Fragments of sub-step ks+1 are read while the MFMAs of ks run,
+        // one column and one row fragment per MFMA group.
+        bf16x8 fa[2][TI], fb[2][TJ];
 #pragma unroll
-            for (int i = 0; i < NTOK; ++i) { tokA[i] = tokB[i]; tokB[i] = tokC[i]; tokC[i] = tn[i]; }
+        for (int i = 0; i < TI; ++i) fa[0][i] = read_a(sC, 0, i);
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) fb[0][j] = read_b(sR, 0, j);
+#pragma unroll
+        for (int ks = 0; ks < BK / 16; ++ks) {
+#pragma unroll
+          for (int i = 0; i < TI; ++i) {
+            const int q = ks * TI + i;
+#pragma unroll
+            for (int o = q * NOPS / NGRP; o < (q + 1) * NOPS / NGRP; ++o) mem_op(o);
+            if (ks + 1 < BK / 16) {
+              fa[(ks + 1) & 1][i] = read_a(sC, ks + 1, i);
+              if (i < TJ) fb[(ks + 1) & 1][i] = read_b(sR, ks + 1, i);
+            }
+#pragma unroll
+            for (int j = 0; j < TJ; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[ks & 1][i], fb[ks & 1][j],
+                                                                  acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
           }
         }
-        const int sb = kt & (NSTAGE - 1);
-        bf16x8 a0[TI], b0[TJ], a1[TI], b1[TJ];
-        read_frags(sb, 0, a0, b0);
-        read_frags(sb, 1, a1, b1);
-        mfmas(a0, b0);
-        mfmas(a1, b1);
+        if constexpr (NTOK > 0) {
+#pragma unroll
+          for (int i = 0; i < NTOK; ++i) tk_a[i] = tn[i];
+        }
       }
     }
 
@@ -489,35 +519,50 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
       }
     } else if constexpr (MODE == G2DX) {
       // d_act tile (bf16) -> d_gate, d_up with gate/up read back from gate_up.
+      // Rows go in batches of RB per thread, all gate/up loads of a batch
+      // issued before any store, so that RB row pairs are in flight.
+      constexpr int RB = 8;
       const int c0 = (tid & 31) * 8;
       const int f = cur.ct * BC + c0;
-#pragma unroll 2
-      for (int row = tid >> 5; row < BR; row += NTHR / 32) {
-        const int r = cur.row0 + row;
-        if (r < cur.row_end && f < I) {
-          const u32x4 dav = *(const u32x4*)(stg + row * SROW + c0);
-          const u32x4 gv = *(const u32x4*)(p.a1 + (int64_t)r * I2 + f);
-          const u32x4 uv = *(const u32x4*)(p.a1 + (int64_t)r * I2 + I + f);
-          u32x4 dgv, duv;
+      const bool fok = f < I;
+#pragma unroll 1
+      for (int rb = tid >> 5; rb < BR; rb += RB * (NTHR / 32)) {
+        u32x4 gv[RB], uv[RB];
 #pragma unroll
-          for (int w = 0; w < 4; ++w) {
-            float dg[2], du[2];
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-              const float da = h ? bf_hi(dav[w]) : bf_lo(dav[w]);
-              const float g = h ? bf_hi(gv[w]) : bf_lo(gv[w]);
-              const float u = h ? bf_hi(uv[w]) : bf_lo(uv[w]);
-              const float sg = sigmoidf_(g);
-              const float s = round_bf(siluf_(g));       // silu(g) as stored in bf16
-              const float ds = round_bf(da * u);          // d silu(g)
-              du[h] = da * s;
-              dg[h] = ds * (sg * (1.f + g * (1.f - sg)));
-            }
-            dgv[w] = pack_bf2(dg[0], dg[1]);
-            duv[w] = pack_bf2(du[0], du[1]);
+        for (int q = 0; q < RB; ++q) {
+          const int r = cur.row0 + rb + q * (NTHR / 32);
+          if (r < cur.row_end && fok) {
+            gv[q] = *(const u32x4*)(p.a1 + (int64_t)r * I2 + f);
+            uv[q] = *(const u32x4*)(p.a1 + (int64_t)r * I2 + I + f);
           }
-          *(u32x4*)(p.out + (int64_t)r * I2 + f) = dgv;
-          *(u32x4*)(p.out + (int64_t)r * I2 + I + f) = duv;
+        }
+#pragma unroll
+        for (int q = 0; q < RB; ++q) {
+          const int row = rb + q * (NTHR / 32);
+          const int r = cur.row0 + row;
+          if (r < cur.row_end && fok) {
+            const u32x4 dav = *(const u32x4*)(stg + row * SROW + c0);
+            u32x4 dgv, duv;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+              float dg[2], du[2];
+#pragma unroll
+              for (int h = 0; h < 2; ++h) {
+                const float da = h ? bf_hi(dav[w]) : bf_lo(dav[w]);
+                const float g = h ? bf_hi(gv[q][w]) : bf_lo(gv[q][w]);
+                const float u = h ? bf_hi(uv[q][w]) : bf_lo(uv[q][w]);
+                const float sg = sigmoidf_(g);
+                const float sl = round_bf(siluf_(g));      // silu(g) as stored in bf16
+                const float ds = round_bf(da * u);          // d silu(g)
+                du[h] = da * sl;
+                dg[h] = ds * (sg * (1.f + g * (1.f - sg)));
+              }
+              dgv[w] = pack_bf2(dg[0], dg[1]);
+              duv[w] = pack_bf2(du[0], du[1]);
+            }
+            *(u32x4*)(p.out + (int64_t)r * I2 + f) = dgv;
+            *(u32x4*)(p.out + (int64_t)r * I2 + I + f) = duv;
+          }
         }
       }
     } else {
@@ -570,7 +615,7 @@ int num_cus() {
 
 template <int MODE, int BR>
 int launch(const GemmArgs& a, int max_tiles, hipStream_t st) {
-  constexpr size_t stages = (size_t)NSTAGE * (BC + BR) * BK * sizeof(bf16);
+  constexpr size_t stages = (size_t)NSLOT * SLOT;
   constexpr size_t staging = (size_t)BR * SROW * sizeof(bf16);
   const size_t lds = stages > staging ? stages : staging;
   if (max_tiles <= 0) return MOE_OK;
