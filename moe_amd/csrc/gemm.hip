@@ -133,6 +133,16 @@ __device__ __forceinline__ int div_topk(int n, uint32_t m, int shift) {
   return (int)(((uint64_t)(uint32_t)n * m) >> shift);
 }
 
+// Logistic sigmoid from the hardware base-2 exponential and reciprocal
+// (v_exp_f32, v_rcp_f32; about 1 ulp each): 1 / (1 + 2^(-x log2 e)).  The
+// epilogues evaluate it once per output element, where an IEEE expf and
+// divide would make them VALU-bound.  The results feed bf16 roundings, so
+// the ulp-level difference to expf/divide shows up only in rare ties.
+// Saturates correctly: x -> -inf gives 0, x -> +inf gives 1.
+__device__ __forceinline__ float fast_sigmoid(float x) {
+  return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(x * -1.44269504088896341f));
+}
+
 template <int MODE, int BR>
 __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
   constexpr bool TOKEN = MODE <= G1DX;                    // rows = routed rows of one expert
@@ -400,11 +410,15 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
     // zeros or in-bounds bytes that are never used) to keep the count exact.
     if (cur.nk > 0) {
       int tk_a[NTOK > 0 ? NTOK : 1], tk_b[NTOK > 0 ? NTOK : 1];
+      // The wait counts rely on issue order; sched_barrier keeps the
+      // scheduler from interleaving the groups.
       fetch_tok(0, tk_a);
       fetch_tok(1, tk_b);
       issue_col(0, tk_a);
+      __builtin_amdgcn_sched_barrier(0);
       fetch_tok(2, tk_a);
       issue_row(0);
+      __builtin_amdgcn_sched_barrier(0);
       issue_col(1, tk_b);
       for (int kt = 0; kt < cur.nk; ++kt) {
         // lgkmcnt(0): this wave's reads of stage kt-1 are complete before
@@ -434,9 +448,11 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
             uint32_t off;
             if constexpr (MODE == G1DW) {
               const int kr = (kt + 2) * BK + km_krow(wid + 4 * i);
-              off = kr < ke_cur - kb_cur
-                        ? (uint32_t)div_topk(tk_a[i], p.tok_mul, p.tok_shift) * (uint32_t)(H * 2) + coff[i]
-                        : kOOB;
+              // Branch-free select (rows past the expert's range read zeros).
+              const uint32_t v =
+                  (uint32_t)div_topk(tk_a[i], p.tok_mul, p.tok_shift) * (uint32_t)(H * 2) + coff[i];
+              const uint32_t m = 0u - (uint32_t)(kr < ke_cur - kb_cur);
+              off = (v & m) | (kOOB & ~m);
             } else {
               off = coff[i] + (uint32_t)(kt + 2) * cstep;
             }
@@ -456,7 +472,10 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
           for (int i = 0; i < TI; ++i) {
             const int q = ks * TI + i;
 #pragma unroll
-            for (int o = q * NOPS / NGRP; o < (q + 1) * NOPS / NGRP; ++o) mem_op(o);
+            for (int o = q * NOPS / NGRP; o < (q + 1) * NOPS / NGRP; ++o) {
+              mem_op(o);
+              if (o + 1 < (q + 1) * NOPS / NGRP) __builtin_amdgcn_sched_barrier(0);
+            }
             if (ks + 1 < BK / 16) {
               fa[(ks + 1) & 1][i] = read_a(sC, ks + 1, i);
               if (i < TJ) fb[(ks + 1) & 1][i] = read_b(sR, ks + 1, i);
@@ -508,7 +527,7 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
           for (int w = 0; w < 4; ++w) {
             const float g0 = bf_lo(gv[w]), g1 = bf_hi(gv[w]);
             const float u0 = bf_lo(uv[w]), u1 = bf_hi(uv[w]);
-            av[w] = pack_bf2(round_bf(siluf_(g0)) * u0, round_bf(siluf_(g1)) * u1);
+            av[w] = pack_bf2(round_bf(g0 * fast_sigmoid(g0)) * u0, round_bf(g1 * fast_sigmoid(g1)) * u1);
           }
           *(u32x4*)(p.out + (int64_t)r * I + f) = av;
           if (p.out2) {
@@ -519,47 +538,54 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
       }
     } else if constexpr (MODE == G2DX) {
       // d_act tile (bf16) -> d_gate, d_up with gate/up read back from gate_up.
-      // Rows go in batches of RB per thread, all gate/up loads of a batch
-      // issued before any store, so that RB row pairs are in flight.
-      constexpr int RB = 8;
+      // Each thread owns NB batches of RB rows; the gate/up loads of batch
+      // b+1 are issued before batch b is computed and stored, so loads never
+      // queue behind this thread's stores.  Loads are clamped in bounds
+      // (rows past the tile's end re-read its last row) and only the stores
+      // are predicated.
+      constexpr int RB = 8, NB = BR / (RB * (NTHR / 32));
       const int c0 = (tid & 31) * 8;
       const int f = cur.ct * BC + c0;
       const bool fok = f < I;
-#pragma unroll 1
-      for (int rb = tid >> 5; rb < BR; rb += RB * (NTHR / 32)) {
-        u32x4 gv[RB], uv[RB];
+      const int fl = fok ? f : 0;
+      const bf16* gsrc = p.a1 + fl;
+      u32x4 gv[2][RB], uv[2][RB];
+      auto load_batch = [&](int b, u32x4 (&g)[RB], u32x4 (&u)[RB]) {
 #pragma unroll
         for (int q = 0; q < RB; ++q) {
-          const int r = cur.row0 + rb + q * (NTHR / 32);
-          if (r < cur.row_end && fok) {
-            gv[q] = *(const u32x4*)(p.a1 + (int64_t)r * I2 + f);
-            uv[q] = *(const u32x4*)(p.a1 + (int64_t)r * I2 + I + f);
-          }
+          const int r = min(cur.row0 + (tid >> 5) + (b * RB + q) * (NTHR / 32), cur.row_end - 1);
+          g[q] = *(const u32x4*)(gsrc + (int64_t)r * I2);
+          u[q] = *(const u32x4*)(gsrc + (int64_t)r * I2 + I);
         }
+      };
+      load_batch(0, gv[0], uv[0]);
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        if (b + 1 < NB) load_batch(b + 1, gv[(b + 1) & 1], uv[(b + 1) & 1]);
 #pragma unroll
         for (int q = 0; q < RB; ++q) {
-          const int row = rb + q * (NTHR / 32);
+          const int row = (tid >> 5) + (b * RB + q) * (NTHR / 32);
           const int r = cur.row0 + row;
-          if (r < cur.row_end && fok) {
-            const u32x4 dav = *(const u32x4*)(stg + row * SROW + c0);
-            u32x4 dgv, duv;
+          const u32x4 dav = *(const u32x4*)(stg + row * SROW + c0);
+          u32x4 dgv, duv;
 #pragma unroll
-            for (int w = 0; w < 4; ++w) {
-              float dg[2], du[2];
+          for (int w = 0; w < 4; ++w) {
+            float dg[2], du[2];
 #pragma unroll
-              for (int h = 0; h < 2; ++h) {
-                const float da = h ? bf_hi(dav[w]) : bf_lo(dav[w]);
-                const float g = h ? bf_hi(gv[q][w]) : bf_lo(gv[q][w]);
-                const float u = h ? bf_hi(uv[q][w]) : bf_lo(uv[q][w]);
-                const float sg = sigmoidf_(g);
-                const float sl = round_bf(siluf_(g));      // silu(g) as stored in bf16
-                const float ds = round_bf(da * u);          // d silu(g)
-                du[h] = da * sl;
-                dg[h] = ds * (sg * (1.f + g * (1.f - sg)));
-              }
-              dgv[w] = pack_bf2(dg[0], dg[1]);
-              duv[w] = pack_bf2(du[0], du[1]);
+            for (int h = 0; h < 2; ++h) {
+              const float da = h ? bf_hi(dav[w]) : bf_lo(dav[w]);
+              const float g = h ? bf_hi(gv[b & 1][q][w]) : bf_lo(gv[b & 1][q][w]);
+              const float u = h ? bf_hi(uv[b & 1][q][w]) : bf_lo(uv[b & 1][q][w]);
+              const float sg = fast_sigmoid(g);
+              const float sl = round_bf(g * sg);          // silu(g) as stored in bf16
+              const float ds = round_bf(da * u);          // d silu(g)
+              du[h] = da * sl;
+              dg[h] = ds * (sg * (1.f + g * (1.f - sg)));
             }
+            dgv[w] = pack_bf2(dg[0], dg[1]);
+            duv[w] = pack_bf2(du[0], du[1]);
+          }
+          if (r < cur.row_end && fok) {
             *(u32x4*)(p.out + (int64_t)r * I2 + f) = dgv;
             *(u32x4*)(p.out + (int64_t)r * I2 + I + f) = duv;
           }
