@@ -116,9 +116,19 @@ __device__ __forceinline__ s16x4 read_tr(const lds_s16x4_t* __restrict__ p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<lds_s16x4_t*>(p));
 }
 
+typedef __attribute__((address_space(3))) char lds_char_t;
+
+// s + v in one VALU add that the optimizer cannot re-associate.
+__device__ __forceinline__ uint32_t opaque_add(uint32_t s, uint32_t v) {
+  uint32_t r;
+  asm("v_add_u32_e32 %0, %1, %2" : "=v"(r) : "s"(s), "v"(v));
+  return r;
+}
+
 // One MFMA fragment (8 consecutive k of one feature) from a k-major stage
-// region: two transpose reads, k 0..3 and k 4..7.
-__device__ __forceinline__ bf16x8 tr_frag(const bf16* p0, const bf16* p1) {
+// region: two transpose reads, k 0..3 and k 4..7.  The addresses stay in the
+// LDS address space so that constant parts fold into the instruction offset.
+__device__ __forceinline__ bf16x8 tr_frag(const lds_char_t* p0, const lds_char_t* p1) {
   const s16x4 lo = read_tr((const lds_s16x4_t*)p0);
   const s16x4 hi = read_tr((const lds_s16x4_t*)p1);
   const s16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
@@ -161,7 +171,8 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
 
   extern __shared__ __attribute__((aligned(16))) bf16 smem[];
 
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: LDS DMA targets stay scalar
   const int wr = wid >> 1, wc = wid & 1;
   const int l32 = lane & 31, hl = lane >> 5;
   const int H = p.H, I = p.I, I2 = 2 * p.I;
@@ -225,10 +236,22 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
   auto km_krow = [&](int blk) { return blk * 2 + (lane >> 5); };
   auto km_chunk = [&](int k) { return (lane & 31) ^ ((k & 3) << 2); };
 
-  __amdgpu_buffer_rsrc_t csrc, rsrc, isrc;
+  // Operand extents: a stage's DMA uses a buffer descriptor rebased to the
+  // stage (base + s*step, bytes - s*step, in scalar registers), so the
+  // per-lane offsets stay fixed and reads past the extent still return 0.
+  const char* cptr = nullptr;
+  const char* rptr = nullptr;
+  uint32_t cbytes = 0, rbytes = 0;
+  __amdgpu_buffer_rsrc_t isrc;
   uint32_t coff[CPW];  // byte offsets of this lane's column blocks at stage 0
   uint32_t roff[RPW];
   uint32_t cstep = 0, rstep = 0;  // byte advance per stage
+  auto stage_rsrc = [&](const char* ptr, uint32_t bytes, uint32_t adv) {
+    // readfirstlane: keep the descriptor scalar (a vector descriptor would
+    // turn every DMA into a waterfall loop).
+    const uint32_t left = __builtin_amdgcn_readfirstlane(adv < bytes ? bytes - adv : 0u);
+    return make_rsrc(ptr + adv, left);
+  };
   int kb_cur = 0, ke_cur = 0;
 
   auto setup = [&](const Tile& d) {
@@ -236,7 +259,8 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
     ke_cur = d.kend;
     // Column operand.
     if constexpr (MODE == G1F) {
-      csrc = make_rsrc(p.w + (int64_t)d.e * I2 * H, (uint32_t)(I2 * H * 2));
+      cptr = (const char*)(p.w + (int64_t)d.e * I2 * H);
+      cbytes = (uint32_t)(I2 * H * 2);
 #pragma unroll
       for (int i = 0; i < CPW; ++i) {
         const int f = kc_feature(wid + 4 * i);  // tile column: [gate 64 | up 64] per wave column
@@ -247,7 +271,8 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
       }
       cstep = BK * 2;
     } else if constexpr (MODE == G2F) {
-      csrc = make_rsrc(p.w + (int64_t)d.e * H * I, (uint32_t)(H * I * 2));
+      cptr = (const char*)(p.w + (int64_t)d.e * H * I);
+      cbytes = (uint32_t)(H * I * 2);
 #pragma unroll
       for (int i = 0; i < CPW; ++i) {
         const int f = kc_feature(wid + 4 * i);
@@ -259,17 +284,20 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
       // k-major column operand: rows of k, features contiguous.
       int ld;
       if constexpr (MODE == G2DX) {
-        csrc = make_rsrc(p.w + (int64_t)d.e * H * I, (uint32_t)(H * I * 2));
+        cptr = (const char*)(p.w + (int64_t)d.e * H * I);
+        cbytes = (uint32_t)(H * I * 2);
         ld = I;
       } else if constexpr (MODE == G1DX) {
-        csrc = make_rsrc(p.w + (int64_t)d.e * I2 * H, (uint32_t)(I2 * H * 2));
+        cptr = (const char*)(p.w + (int64_t)d.e * I2 * H);
+        cbytes = (uint32_t)(I2 * H * 2);
         ld = H;
       } else if constexpr (MODE == G2DW) {
-        csrc = make_rsrc(p.a1 + (int64_t)d.kbeg * I,
-                         (uint32_t)((int64_t)(d.kend - d.kbeg) * I * 2));
+        cptr = (const char*)(p.a1 + (int64_t)d.kbeg * I);
+        cbytes = (uint32_t)((int64_t)(d.kend - d.kbeg) * I * 2);
         ld = I;
       } else {  // G1DW: rows of hidden_states gathered through row_src
-        csrc = make_rsrc(p.x, (uint32_t)(p.T * H * 2));
+        cptr = (const char*)p.x;
+        cbytes = (uint32_t)(p.T * H * 2);
         ld = H;
       }
 #pragma unroll
@@ -282,7 +310,8 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
     }
     // Row operand.
     if constexpr (MODE == G1F) {
-      rsrc = make_rsrc(p.x, (uint32_t)(p.T * H * 2));
+      rptr = (const char*)p.x;
+      rbytes = (uint32_t)(p.T * H * 2);
 #pragma unroll
       for (int i = 0; i < RPW; ++i) {
         const int f = kc_feature(wid + 4 * i);
@@ -293,8 +322,8 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
       rstep = BK * 2;
     } else if constexpr (TOKEN) {
       const int ld = (MODE == G2F) ? I : (MODE == G2DX ? H : I2);
-      rsrc = make_rsrc(p.a0 + (int64_t)d.row0 * ld,
-                       (uint32_t)((int64_t)(d.row_end - d.row0) * ld * 2));
+      rptr = (const char*)(p.a0 + (int64_t)d.row0 * ld);
+      rbytes = (uint32_t)((int64_t)(d.row_end - d.row0) * ld * 2);
 #pragma unroll
       for (int i = 0; i < RPW; ++i) {
         const int f = kc_feature(wid + 4 * i);
@@ -304,8 +333,8 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
       rstep = BK * 2;
     } else {
       const int ld = (MODE == G2DW) ? H : I2;
-      rsrc = make_rsrc(p.a0 + (int64_t)d.kbeg * ld,
-                       (uint32_t)((int64_t)(d.kend - d.kbeg) * ld * 2));
+      rptr = (const char*)(p.a0 + (int64_t)d.kbeg * ld);
+      rbytes = (uint32_t)((int64_t)(d.kend - d.kbeg) * ld * 2);
 #pragma unroll
       for (int i = 0; i < RPW; ++i) {
         const int k = km_krow(wid + 4 * i);
@@ -332,58 +361,84 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
   auto slot_ptr = [&](int h) { return (char*)smem + (h % NSLOT) * SLOT; };
 
   // DMA of the column half of stage s (ring position 2s).
+  auto col_off = [&](int s, int i, const int (&tk)[NTOK > 0 ? NTOK : 1]) -> uint32_t {
+    if constexpr (MODE == G1DW) {
+      const int kr = s * BK + km_krow(wid + 4 * i);
+      // Branch-free select (rows past the expert's range read zeros).
+      const uint32_t v = (uint32_t)div_topk(tk[i], p.tok_mul, p.tok_shift) * (uint32_t)(H * 2) + coff[i];
+      const uint32_t m = 0u - (uint32_t)(kr < ke_cur - kb_cur);
+      return (v & m) | (kOOB & ~m);
+    } else {
+      return coff[i];
+    }
+  };
   auto issue_col = [&](int s, const int (&tk)[NTOK > 0 ? NTOK : 1]) {
     char* base = slot_ptr(2 * s);
+    const auto rs = stage_rsrc(cptr, cbytes, (uint32_t)s * cstep);
 #pragma unroll
-    for (int i = 0; i < CPW; ++i) {
-      uint32_t off;
-      if constexpr (MODE == G1DW) {
-        const int kr = s * BK + km_krow(wid + 4 * i);
-        off = kr < ke_cur - kb_cur
-                  ? (uint32_t)div_topk(tk[i], p.tok_mul, p.tok_shift) * (uint32_t)(H * 2) + coff[i]
-                  : kOOB;
-      } else {
-        off = coff[i] + (uint32_t)s * cstep;
-      }
-      dma16(csrc, off, base + (wid + 4 * i) * 1024);
-    }
+    for (int i = 0; i < CPW; ++i) dma16(rs, col_off(s, i, tk), base + (wid + 4 * i) * 1024);
   };
   // DMA of the row half of stage s (ring position 2s+1).
   auto issue_row = [&](int s) {
     char* base = slot_ptr(2 * s + 1);
+    const auto rs = stage_rsrc(rptr, rbytes, (uint32_t)s * rstep);
 #pragma unroll
-    for (int i = 0; i < RPW; ++i)
-      dma16(rsrc, roff[i] + (uint32_t)s * rstep, base + (wid + 4 * i) * 1024);
+    for (int i = 0; i < RPW; ++i) dma16(rs, roff[i], base + (wid + 4 * i) * 1024);
   };
 
-  // Fragment reads of k sub-step ks (16 k) from the column / row slots:
-  // column sub-tile i, row sub-tile j.
-  auto read_a = [&](const bf16* sC, int ks, int i) -> bf16x8 {
-    if constexpr (!COL_KM) {
-      const int f = wc * 128 + i * 32 + l32;
-      const int c = (2 * ks + hl) ^ ((f >> 1) & 7);
-      return *(const bf16x8*)(sC + f * BK + c * 8);
-    } else {
-      const int g = lane >> 4, jj = lane & 15;
-      const int ka = ks * 16 + 8 * (g >> 1) + (jj >> 2), kb = ka + 4;  // transpose-read k rows
-      const int n = wc * 128 + i * 32 + 16 * (g & 1) + 4 * (jj & 3);
-      const bf16* pa = sC + ka * BC + (((n >> 3) ^ ((ka & 3) << 2)) << 3) + (n & 4);
-      const bf16* pb = sC + kb * BC + (((n >> 3) ^ ((kb & 3) << 2)) << 3) + (n & 4);
-      return tr_frag(pa, pb);
+  // Fragment reads.  Per-lane byte offsets within a slot are computed once:
+  // k-contiguous operands need one base per k sub-step ks (the swizzle
+  // mixes ks into the chunk index) and step 4096 bytes per 32-row sub-tile;
+  // k-major operands need one base per sub-tile (the swizzle mixes the
+  // sub-tile into the chunk index) and step 8192 bytes per ks and 2048 per
+  // transpose half.  A read then costs one add of the slot's base.
+  const int tg = lane >> 4, tj = lane & 15;
+  const int tka = 8 * (tg >> 1) + (tj >> 2);                  // transpose-read k row (ks 0, half 0)
+  const int tsub = 2 * (tg & 1) + ((tj & 3) >> 1);            // chunk within a 32-feature group
+  const uint32_t thalf = 8 * (tj & 1);                        // byte half within the chunk
+  uint32_t a_off[4], b_off[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    if constexpr (!COL_KM)
+      a_off[q] = (uint32_t)(wc * 128 + l32) * (BK * 2) + (uint32_t)(((2 * q + hl) ^ ((l32 >> 1) & 7)) * 16);
+    else
+      a_off[q] = (uint32_t)tka * (BC * 2) +
+                 ((uint32_t)((wc * 16 + q * 4 + tsub) ^ ((tka & 3) << 2)) << 4) + thalf;
+    if constexpr (!ROW_KM)
+      b_off[q] = (uint32_t)(wr * WR + l32) * (BK * 2) + (uint32_t)(((2 * q + hl) ^ ((l32 >> 1) & 7)) * 16);
+    else
+      b_off[q] = (uint32_t)tka * (BR * 2) +
+                 ((uint32_t)((wr * (WR / 8) + q * 4 + tsub) ^ ((tka & 3) << 2)) << 4) + thalf;
+  }
+  // Column sub-tile i / row sub-tile j of k sub-step ks from the slot at
+  // byte offset so.
+  // Per step, the slot base is added to the four per-lane offsets of each
+  // operand once (opaque to the optimizer, which would otherwise fold the
+  // sub-step constants into the scalar slot base and re-add per read); the
+  // sub-step and sub-tile parts then ride in the instructions' offsets.
+  const lds_char_t* const lds0 = (const lds_char_t*)smem;
+  uint32_t a_adr[4], b_adr[4];
+  auto slot_bases = [&](uint32_t sC, uint32_t sR) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      a_adr[q] = opaque_add(sC, a_off[q]);
+      b_adr[q] = opaque_add(sR, b_off[q]);
     }
   };
-  auto read_b = [&](const bf16* sR, int ks, int j) -> bf16x8 {
-    if constexpr (!ROW_KM) {
-      const int f = wr * WR + j * 32 + l32;
-      const int c = (2 * ks + hl) ^ ((f >> 1) & 7);
-      return *(const bf16x8*)(sR + f * BK + c * 8);
+  auto read_a = [&](int ks, int i) -> bf16x8 {
+    if constexpr (!COL_KM) {
+      return *(const __attribute__((address_space(3))) bf16x8*)(lds0 + a_adr[ks] + i * 4096);
     } else {
-      const int g = lane >> 4, jj = lane & 15;
-      const int ka = ks * 16 + 8 * (g >> 1) + (jj >> 2), kb = ka + 4;
-      const int n = wr * WR + j * 32 + 16 * (g & 1) + 4 * (jj & 3);
-      const bf16* pa = sR + ka * BR + (((n >> 3) ^ ((ka & 3) << 2)) << 3) + (n & 4);
-      const bf16* pb = sR + kb * BR + (((n >> 3) ^ ((kb & 3) << 2)) << 3) + (n & 4);
-      return tr_frag(pa, pb);
+      const lds_char_t* q = lds0 + a_adr[i] + ks * (16 * BC * 2);
+      return tr_frag(q, q + 4 * BC * 2);
+    }
+  };
+  auto read_b = [&](int ks, int j) -> bf16x8 {
+    if constexpr (!ROW_KM) {
+      return *(const __attribute__((address_space(3))) bf16x8*)(lds0 + b_adr[ks] + j * 4096);
+    } else {
+      const lds_char_t* q = lds0 + b_adr[j] + ks * (16 * BR * 2);
+      return tr_frag(q, q + 4 * BR * 2);
     }
   };
 
@@ -425,8 +480,8 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
         // the barrier lets other waves overwrite their slots.
         WAIT_VMCNT_LGKM0(CPW);
         __builtin_amdgcn_s_barrier();
-        const bf16* sC = (const bf16*)slot_ptr(2 * kt);
-        const bf16* sR = (const bf16*)slot_ptr(2 * kt + 1);
+        const uint32_t sC = (uint32_t)((2 * kt) % NSLOT) * SLOT;      // column slot (bytes)
+        const uint32_t sR = (uint32_t)((2 * kt + 1) % NSLOT) * SLOT;  // row slot
         char* rdst = slot_ptr(2 * kt + 3);  // row half of stage kt+1
         char* cdst = slot_ptr(2 * kt + 4);  // column half of stage kt+2
         int tn[NTOK > 0 ? NTOK : 1];
@@ -434,6 +489,8 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
         // the row half of kt+1, DMA of the column half of kt+2, in this
         // order) are spread over its 16 MFMA groups: issued in one burst
         // they back up the texture pipe and stall the wave's MFMA issue.
+        const auto rs_row = stage_rsrc(rptr, rbytes, (uint32_t)(kt + 1) * rstep);
+        const auto rs_col = stage_rsrc(cptr, cbytes, (uint32_t)(kt + 2) * cstep);
         auto mem_op = [&](int o) {
           if (o < NTOK) {
             if constexpr (MODE == G1DW) {
@@ -442,30 +499,20 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
             }
           } else if (o < NTOK + RPW) {
             const int i = o - NTOK;
-            dma16(rsrc, roff[i] + (uint32_t)(kt + 1) * rstep, rdst + (wid + 4 * i) * 1024);
+            dma16(rs_row, roff[i], rdst + (wid + 4 * i) * 1024);
           } else {
             const int i = o - NTOK - RPW;
-            uint32_t off;
-            if constexpr (MODE == G1DW) {
-              const int kr = (kt + 2) * BK + km_krow(wid + 4 * i);
-              // Branch-free select (rows past the expert's range read zeros).
-              const uint32_t v =
-                  (uint32_t)div_topk(tk_a[i], p.tok_mul, p.tok_shift) * (uint32_t)(H * 2) + coff[i];
-              const uint32_t m = 0u - (uint32_t)(kr < ke_cur - kb_cur);
-              off = (v & m) | (kOOB & ~m);
-            } else {
-              off = coff[i] + (uint32_t)(kt + 2) * cstep;
-            }
-            dma16(csrc, off, cdst + (wid + 4 * i) * 1024);
+            dma16(rs_col, col_off(kt + 2, i, tk_a), cdst + (wid + 4 * i) * 1024);
           }
         };
         // Fragments of sub-step ks+1 are read while the MFMAs of ks run,
         // one column and one row fragment per MFMA group.
         bf16x8 fa[2][TI], fb[2][TJ];
+        slot_bases(sC, sR);
 #pragma unroll
-        for (int i = 0; i < TI; ++i) fa[0][i] = read_a(sC, 0, i);
+        for (int i = 0; i < TI; ++i) fa[0][i] = read_a(0, i);
 #pragma unroll
-        for (int j = 0; j < TJ; ++j) fb[0][j] = read_b(sR, 0, j);
+        for (int j = 0; j < TJ; ++j) fb[0][j] = read_b(0, j);
 #pragma unroll
         for (int ks = 0; ks < BK / 16; ++ks) {
 #pragma unroll
@@ -477,8 +524,8 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
               if (o + 1 < (q + 1) * NOPS / NGRP) __builtin_amdgcn_sched_barrier(0);
             }
             if (ks + 1 < BK / 16) {
-              fa[(ks + 1) & 1][i] = read_a(sC, ks + 1, i);
-              if (i < TJ) fb[(ks + 1) & 1][i] = read_b(sR, ks + 1, i);
+              fa[(ks + 1) & 1][i] = read_a(ks + 1, i);
+              if (i < TJ) fb[(ks + 1) & 1][i] = read_b(ks + 1, i);
             }
 #pragma unroll
             for (int j = 0; j < TJ; ++j)
