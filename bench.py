@@ -88,6 +88,33 @@ def cpu_baseline(cfg, tokens: int) -> dict:
                       f"I={c.I}, bf16-emulating fp32 math), 1 fwd+bwd, {dt:.1f} s; CPU: {model}"}
 
 
+def copy_calibration(nbytes: int) -> None:
+    """A plain copy of known size: reads nbytes, writes nbytes per launch."""
+    src = torch.ones(nbytes, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": nbytes, "launches": 3}), flush=True)
+
+
+def recorded_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` as measured by rocprofv3 FETCH_SIZE and
+    WRITE_SIZE counters (scaled by the copy calibration) and recorded in
+    profiles/gemm_hbm_traffic_L.md as `traffic_bytes_per_launch[<kernel>] = N`."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        "gemm_hbm_traffic_L.md")
+    try:
+        for line in open(path):
+            line = line.strip().strip("`")
+            if line.startswith(f"traffic_bytes_per_launch[{kernel}]"):
+                return float(line.split("=", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -96,7 +123,13 @@ def main():
     ap.add_argument("--config", default="l")
     ap.add_argument("--cpu-tokens", type=int, default=16384)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                    help="only run a plain device-to-device copy of BYTES (three times): the "
+                         "known-size kernel that scales the FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU's share of the layer; runs on more than one GPU "
@@ -194,7 +227,7 @@ def main():
         "roofline": {"bound": "mfma", "kernel": dom.replace("moe_amd_", ""),
                      "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": None},
+                     "traffic": recorded_traffic(dom.replace("moe_amd_", ""))},
         "kernels": kernels,
     }
     if not args.no_cpu_baseline:
