@@ -61,7 +61,12 @@ constexpr int BK = 64;       // k per stage
 constexpr int SLOT = 32768;  // bytes per LDS slot (one operand's half of a stage)
 constexpr int NSLOT = 5;     // ring of half-stages: two consumed, three in flight
 constexpr int BC = 256;    // output columns per workgroup
-constexpr int NTHR = 256;  // 4 waves
+// Waves per workgroup, as NW/2 row groups x 2 column groups.  Four waves (one
+// per SIMD, 128x128 per wave at BR = 256) measured faster on MI355X than
+// eight (two per SIMD, 64x128 per wave), which trade latency hiding for 1.5x
+// the LDS fragment traffic.
+template <int BR>
+constexpr int kWaves = 4;
 constexpr int SROW = 260;  // bf16 per row of the epilogue staging tile (520 B: conflict-free)
 
 enum Mode { G1F = 0, G2F = 1, G2DX = 2, G1DX = 3, G2DW = 4, G1DW = 5 };
@@ -154,19 +159,21 @@ __device__ __forceinline__ float fast_sigmoid(float x) {
 }
 
 template <int MODE, int BR>
-__global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
+__global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmArgs p) {
+  constexpr int NW = kWaves<BR>;                          // waves, as NW/2 rows x 2 columns
+  constexpr int NTHR = NW * 64;
   constexpr bool TOKEN = MODE <= G1DX;                    // rows = routed rows of one expert
   constexpr bool COL_KM = !(MODE == G1F || MODE == G2F);  // column operand k-major in memory
   constexpr bool ROW_KM = !TOKEN;                         // row operand k-major (dW)
-  constexpr int WR = BR / 2;                              // rows per wave
+  constexpr int WR = BR / (NW / 2);                       // rows per wave
   constexpr int TJ = WR / 32;                             // MFMA row sub-tiles per wave
   constexpr int TI = 4;                                   // MFMA col sub-tiles per wave (128 cols)
-  constexpr int CPW = BC * BK * 2 / 1024 / 4;             // 1 KB DMA blocks per wave, column half
-  constexpr int RPW = BR * BK * 2 / 1024 / 4;             // ... row half
+  constexpr int CPW = BC * BK * 2 / 1024 / NW;            // 1 KB DMA blocks per wave, column half
+  constexpr int RPW = BR * BK * 2 / 1024 / NW;            // ... row half
   constexpr int NTOK = (MODE == G1DW) ? CPW : 0;          // gathered-row indices per lane and stage
   constexpr int NOPS = NTOK + RPW + CPW;                  // memory ops per main-loop step
   constexpr int NGRP = (BK / 16) * TI;                    // MFMA groups per step
-  static_assert(CPW == 8 && RPW * 32 == BR, "DMA blocks per wave");
+  static_assert(CPW * NW == 32 && RPW * NW * 8 == BR && TJ >= 1, "DMA blocks per wave");
   static_assert(TOKEN || BR == 256, "dW modes use 256-row tiles");
 
   extern __shared__ __attribute__((aligned(16))) bf16 smem[];
@@ -226,7 +233,7 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
   };
 
   // ------------------------------------------------------- DMA geometry
-  // Wave w fills the 1 KB blocks w, w+4, w+8, ... of each half-stage.  In a
+  // Wave w fills the 1 KB blocks w, w+NW, w+2NW, ... of each half-stage.  In a
   // k-contiguous half, lane L carries feature 8*blk + L/8 and physical chunk
   // L&7, which holds logical chunk (L&7) ^ ((feature>>1)&7).  In a k-major
   // half it carries k row 2*blk + L/32 and physical chunk L&31, which holds
@@ -263,7 +270,7 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
       cbytes = (uint32_t)(I2 * H * 2);
 #pragma unroll
       for (int i = 0; i < CPW; ++i) {
-        const int f = kc_feature(wid + 4 * i);  // tile column: [gate 64 | up 64] per wave column
+        const int f = kc_feature(wid + NW * i);  // tile column: [gate 64 | up 64] per wave column
         const int lc = f & 127;
         const int feat = d.ct * 128 + (f >> 7) * 64 + (lc & 63);
         const int wrow = (lc < 64) ? feat : I + feat;
@@ -275,7 +282,7 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
       cbytes = (uint32_t)(H * I * 2);
 #pragma unroll
       for (int i = 0; i < CPW; ++i) {
-        const int f = kc_feature(wid + 4 * i);
+        const int f = kc_feature(wid + NW * i);
         const int wrow = d.ct * BC + f;
         coff[i] = wrow < H ? (uint32_t)wrow * (uint32_t)(I * 2) + kc_chunk(f) * 16 : kOOB;
       }
@@ -302,7 +309,7 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
       }
 #pragma unroll
       for (int i = 0; i < CPW; ++i) {
-        const int k = km_krow(wid + 4 * i);
+        const int k = km_krow(wid + NW * i);
         const uint32_t fb = (uint32_t)(d.ct * BC + km_chunk(k) * 8) * 2;
         coff[i] = (MODE == G1DW) ? fb : (uint32_t)k * (uint32_t)(ld * 2) + fb;
       }
@@ -314,7 +321,7 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
       rbytes = (uint32_t)(p.T * H * 2);
 #pragma unroll
       for (int i = 0; i < RPW; ++i) {
-        const int f = kc_feature(wid + 4 * i);
+        const int f = kc_feature(wid + NW * i);
         const int r = min(d.row0 + f, d.row_end - 1);
         const int tok = div_topk(p.row_src[r], p.tok_mul, p.tok_shift);
         roff[i] = (uint32_t)tok * (uint32_t)(H * 2) + kc_chunk(f) * 16;
@@ -326,7 +333,7 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
       rbytes = (uint32_t)((int64_t)(d.row_end - d.row0) * ld * 2);
 #pragma unroll
       for (int i = 0; i < RPW; ++i) {
-        const int f = kc_feature(wid + 4 * i);
+        const int f = kc_feature(wid + NW * i);
         const int r = min(f, d.row_end - d.row0 - 1);
         roff[i] = (uint32_t)r * (uint32_t)(ld * 2) + kc_chunk(f) * 16;
       }
@@ -337,7 +344,7 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
       rbytes = (uint32_t)((int64_t)(d.kend - d.kbeg) * ld * 2);
 #pragma unroll
       for (int i = 0; i < RPW; ++i) {
-        const int k = km_krow(wid + 4 * i);
+        const int k = km_krow(wid + NW * i);
         roff[i] = (uint32_t)k * (uint32_t)(ld * 2) + (uint32_t)(d.row0 + km_chunk(k) * 8) * 2;
       }
       rstep = (uint32_t)BK * ld * 2;
@@ -352,7 +359,7 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
     if constexpr (MODE == G1DW) {
 #pragma unroll
       for (int i = 0; i < NTOK; ++i) {
-        const int kr = s * BK + km_krow(wid + 4 * i);
+        const int kr = s * BK + km_krow(wid + NW * i);
         tk[i] = __builtin_amdgcn_raw_buffer_load_b32(isrc, (uint32_t)(kb_cur + kr) * 4, 0, 0);
       }
     }
@@ -363,7 +370,7 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
   // DMA of the column half of stage s (ring position 2s).
   auto col_off = [&](int s, int i, const int (&tk)[NTOK > 0 ? NTOK : 1]) -> uint32_t {
     if constexpr (MODE == G1DW) {
-      const int kr = s * BK + km_krow(wid + 4 * i);
+      const int kr = s * BK + km_krow(wid + NW * i);
       // Branch-free select (rows past the expert's range read zeros).
       const uint32_t v = (uint32_t)div_topk(tk[i], p.tok_mul, p.tok_shift) * (uint32_t)(H * 2) + coff[i];
       const uint32_t m = 0u - (uint32_t)(kr < ke_cur - kb_cur);
@@ -376,14 +383,14 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
     char* base = slot_ptr(2 * s);
     const auto rs = stage_rsrc(cptr, cbytes, (uint32_t)s * cstep);
 #pragma unroll
-    for (int i = 0; i < CPW; ++i) dma16(rs, col_off(s, i, tk), base + (wid + 4 * i) * 1024);
+    for (int i = 0; i < CPW; ++i) dma16(rs, col_off(s, i, tk), base + (wid + NW * i) * 1024);
   };
   // DMA of the row half of stage s (ring position 2s+1).
   auto issue_row = [&](int s) {
     char* base = slot_ptr(2 * s + 1);
     const auto rs = stage_rsrc(rptr, rbytes, (uint32_t)s * rstep);
 #pragma unroll
-    for (int i = 0; i < RPW; ++i) dma16(rs, roff[i], base + (wid + 4 * i) * 1024);
+    for (int i = 0; i < RPW; ++i) dma16(rs, roff[i], base + (wid + NW * i) * 1024);
   };
 
   // Fragment reads.  Per-lane byte offsets within a slot are computed once:
@@ -494,15 +501,15 @@ __global__ __launch_bounds__(NTHR, 1) void grouped_gemm_kernel(GemmArgs p) {
         auto mem_op = [&](int o) {
           if (o < NTOK) {
             if constexpr (MODE == G1DW) {
-              const int kr = (kt + 3) * BK + km_krow(wid + 4 * o);
+              const int kr = (kt + 3) * BK + km_krow(wid + NW * o);
               tn[o] = __builtin_amdgcn_raw_buffer_load_b32(isrc, (uint32_t)(kb_cur + kr) * 4, 0, 0);
             }
           } else if (o < NTOK + RPW) {
             const int i = o - NTOK;
-            dma16(rs_row, roff[i], rdst + (wid + 4 * i) * 1024);
+            dma16(rs_row, roff[i], rdst + (wid + NW * i) * 1024);
           } else {
             const int i = o - NTOK - RPW;
-            dma16(rs_col, col_off(kt + 2, i, tk_a), cdst + (wid + 4 * i) * 1024);
+            dma16(rs_col, col_off(kt + 2, i, tk_a), cdst + (wid + NW * i) * 1024);
           }
         };
         // Fragments of sub-step ks+1 are read while the MFMAs of ks run,
@@ -704,7 +711,7 @@ int launch(const GemmArgs& a, int max_tiles, hipStream_t st) {
   const int need = (max_tiles + 7) / 8 * 8;
   if (grid > need) grid = need;
   if (grid < 8) grid = 8;
-  grouped_gemm_kernel<MODE, BR><<<grid, NTHR, lds, st>>>(a);
+  grouped_gemm_kernel<MODE, BR><<<grid, kWaves<BR> * 64, lds, st>>>(a);
   return check_launch("grouped_gemm");
 }
 
