@@ -566,27 +566,41 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
         }
     __syncthreads();
     if constexpr (MODE == G1F) {
-      // 128 output features per tile; 16 lanes x 8 features per row.
+      // 128 output features per tile; 16 lanes x 8 features per row, in
+      // batches of RB rows (LDS reads first, then math and stores).
       const int fl = (tid & 15) * 8;
       const int scol = (fl >> 6) * 128 + (fl & 63);  // gate column in the staging tile
       const int f = cur.ct * 128 + fl;
-#pragma unroll 4
-      for (int row = tid >> 4; row < BR; row += NTHR / 16) {
-        const int r = cur.row0 + row;
-        if (r < cur.row_end && f < I) {
-          const u32x4 gv = *(const u32x4*)(stg + row * SROW + scol);
-          const u32x4 uv = *(const u32x4*)(stg + row * SROW + scol + 64);
+      const bool fok = f < I;
+      constexpr int RPT = BR / (NTHR / 16);  // rows per thread
+      constexpr int RB = RPT < 8 ? RPT : 8, NB = RPT / RB;
+      static_assert(NB * RB * (NTHR / 16) == BR, "epilogue batches");
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        u32x4 gv[RB], uv[RB];
+#pragma unroll
+        for (int q = 0; q < RB; ++q) {
+          const int row = (tid >> 4) + (b * RB + q) * (NTHR / 16);
+          gv[q] = *(const u32x4*)(stg + row * SROW + scol);
+          uv[q] = *(const u32x4*)(stg + row * SROW + scol + 64);
+        }
+#pragma unroll
+        for (int q = 0; q < RB; ++q) {
+          const int row = (tid >> 4) + (b * RB + q) * (NTHR / 16);
+          const int r = cur.row0 + row;
           u32x4 av;
 #pragma unroll
           for (int w = 0; w < 4; ++w) {
-            const float g0 = bf_lo(gv[w]), g1 = bf_hi(gv[w]);
-            const float u0 = bf_lo(uv[w]), u1 = bf_hi(uv[w]);
+            const float g0 = bf_lo(gv[q][w]), g1 = bf_hi(gv[q][w]);
+            const float u0 = bf_lo(uv[q][w]), u1 = bf_hi(uv[q][w]);
             av[w] = pack_bf2(round_bf(g0 * fast_sigmoid(g0)) * u0, round_bf(g1 * fast_sigmoid(g1)) * u1);
           }
-          *(u32x4*)(p.out + (int64_t)r * I + f) = av;
-          if (p.out2) {
-            *(u32x4*)(p.out2 + (int64_t)r * I2 + f) = gv;
-            *(u32x4*)(p.out2 + (int64_t)r * I2 + I + f) = uv;
+          if (r < cur.row_end && fok) {
+            *(u32x4*)(p.out + (int64_t)r * I + f) = av;
+            if (p.out2) {
+              *(u32x4*)(p.out2 + (int64_t)r * I2 + f) = gv[q];
+              *(u32x4*)(p.out2 + (int64_t)r * I2 + I + f) = uv[q];
+            }
           }
         }
       }
@@ -660,11 +674,26 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
         ld = (MODE == G2DW) ? I : H;
         obase = p.out + (int64_t)cur.e * (MODE == G2DW ? (int64_t)H * I : (int64_t)I2 * H);
       }
-#pragma unroll 4
-      for (int row = tid >> 5; row < BR; row += NTHR / 32) {
-        const int r = cur.row0 + row;
-        if (r < nrows && f < ld)
-          *(u32x4*)(obase + (int64_t)r * ld + f) = *(const u32x4*)(stg + row * SROW + c0);
+      // Batches of RB rows: all LDS reads of a batch first, then its stores,
+      // so the LDS latency is paid once per batch rather than per row.
+      constexpr int RPT = BR / (NTHR / 32);  // rows per thread
+      constexpr int RB = RPT < 16 ? RPT : 16, NB = RPT / RB;
+      static_assert(NB * RB * (NTHR / 32) == BR, "epilogue batches");
+      const bool fok = f < ld;
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        u32x4 v[RB];
+#pragma unroll
+        for (int q = 0; q < RB; ++q) {
+          const int row = (tid >> 5) + (b * RB + q) * (NTHR / 32);
+          v[q] = *(const u32x4*)(stg + row * SROW + c0);
+        }
+#pragma unroll
+        for (int q = 0; q < RB; ++q) {
+          const int row = (tid >> 5) + (b * RB + q) * (NTHR / 32);
+          const int r = cur.row0 + row;
+          if (r < nrows && fok) *(u32x4*)(obase + (int64_t)r * ld + f) = v[q];
+        }
       }
     }
     __syncthreads();  // staging reads done before the next tile's stages land
