@@ -55,6 +55,17 @@ const char* moe_amd_last_error(void);
 
 /* ---------------------------------------------------------------- router */
 
+/* The gating linear: logits[T,E] = hidden_states[T,H] . weight[E,H]^T with
+ * bf16 inputs and fp32 accumulation (MFMA).  logits_dtype BF16 rounds the
+ * result to bf16, as F.linear on bf16 tensors does for the softmax router
+ * (Qwen3MoeTopKRouter.forward, src/models/modeling_qwen3_moe.py:268-270);
+ * F32 keeps the fp32 sums, which is F.linear(h.float(), W.float()) of the
+ * DeepSeek router (src/models/router.py:107-109) -- a bf16 x bf16 product is
+ * exact in fp32, so only the summation order differs.  H multiple of 64,
+ * E multiple of 8. */
+int moe_amd_router_linear(const void* hidden_states, const void* weight, int64_t T, int E, int H,
+                          void* logits, int logits_dtype, void* stream);
+
 /* Softmax router after the gating linear: probs = softmax(float(logits) +
  * logit_offset) over E, top-K (value descending, lower expert id first on
  * equal values), optional renormalisation by the top-K sum (no epsilon).

@@ -36,6 +36,7 @@ _sz = ctypes.c_size_t
 SIGNATURES: dict[str, tuple] = {
     "moe_amd_abi_version": (_i, []),
     "moe_amd_last_error": (ctypes.c_char_p, []),
+    "moe_amd_router_linear": (_i, [_p, _p, _i64, _i, _i, _p, _i, _p]),
     "moe_amd_router_softmax_topk": (_i, [_p, _i, _p, _i64, _i, _i, _i, _p, _p, _p, _p, _p]),
     "moe_amd_router_softmax_topk_backward": (_i, [_p, _p, _p, _p, _i64, _i, _i, _i, _p, _i, _p]),
     "moe_amd_router_sigmoid_topk": (

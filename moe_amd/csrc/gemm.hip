@@ -69,7 +69,8 @@ template <int BR>
 constexpr int kWaves = 4;
 constexpr int SROW = 260;  // bf16 per row of the epilogue staging tile (520 B: conflict-free)
 
-enum Mode { G1F = 0, G2F = 1, G2DX = 2, G1DX = 3, G2DW = 4, G1DW = 5 };
+// RL: the router's dense linear, logits[T, E] = x[T, H] . W_r[E, H]^T.
+enum Mode { G1F = 0, G2F = 1, G2DX = 2, G1DX = 3, G2DW = 4, G1DW = 5, RL = 6 };
 
 struct GemmArgs {
   const bf16* x;         // hidden_states [T,H]
@@ -82,6 +83,7 @@ struct GemmArgs {
   const int4* tile_info; // token modes: {expert, first row, end row, 0} per row tile
   bf16* out;
   bf16* out2;            // gate_up output of G1F (may be null)
+  float* out_f32;        // RL: fp32 logits (null: bf16 logits in out)
   int64_t T, S;
   int E, H, I, topk;
   uint32_t tok_mul;      // n / topk == (n * tok_mul) >> tok_shift for 0 <= n < 2^31
@@ -163,8 +165,9 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
   constexpr int NW = kWaves<BR>;                          // waves, as NW/2 rows x 2 columns
   constexpr int NTHR = NW * 64;
   constexpr bool TOKEN = MODE <= G1DX;                    // rows = routed rows of one expert
-  constexpr bool COL_KM = !(MODE == G1F || MODE == G2F);  // column operand k-major in memory
-  constexpr bool ROW_KM = !TOKEN;                         // row operand k-major (dW)
+  constexpr bool DENSE = MODE == RL;                      // rows = all T tokens, one "expert"
+  constexpr bool COL_KM = !(MODE == G1F || MODE == G2F || DENSE);  // column operand k-major
+  constexpr bool ROW_KM = !TOKEN && !DENSE;               // row operand k-major (dW)
   constexpr int WR = BR / (NW / 2);                       // rows per wave
   constexpr int TJ = WR / 32;                             // MFMA row sub-tiles per wave
   constexpr int TI = 4;                                   // MFMA col sub-tiles per wave (128 cols)
@@ -174,7 +177,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
   constexpr int NOPS = NTOK + RPW + CPW;                  // memory ops per main-loop step
   constexpr int NGRP = (BK / 16) * TI;                    // MFMA groups per step
   static_assert(CPW * NW == 32 && RPW * NW * 8 == BR && TJ >= 1, "DMA blocks per wave");
-  static_assert(TOKEN || BR == 256, "dW modes use 256-row tiles");
+  static_assert(TOKEN || DENSE || BR == 256, "dW modes use 256-row tiles");
 
   extern __shared__ __attribute__((aligned(16))) bf16 smem[];
 
@@ -204,6 +207,12 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       d.row0 = ti.y;
       d.row_end = ti.z;
       d.kbeg = d.kend = 0;
+    } else if constexpr (DENSE) {
+      d.ct = tt % p.n_ct;
+      d.e = 0;
+      d.row0 = (tt / p.n_ct) * BR;
+      d.row_end = (int)min((int64_t)d.row0 + BR, p.T);
+      d.kbeg = d.kend = 0;
     } else {
       const int per_e = p.n_rt * p.n_ct;
       d.e = tt / per_e;
@@ -224,7 +233,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
     d.kbeg = __builtin_amdgcn_readfirstlane(d.kbeg);
     d.kend = __builtin_amdgcn_readfirstlane(d.kend);
     int K_len;
-    if constexpr (MODE == G1F || MODE == G2DX) K_len = H;
+    if constexpr (MODE == G1F || MODE == G2DX || DENSE) K_len = H;
     else if constexpr (MODE == G2F) K_len = I;
     else if constexpr (MODE == G1DX) K_len = I2;
     else K_len = d.kend - d.kbeg;
@@ -277,14 +286,16 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
         coff[i] = (uint32_t)wrow * (uint32_t)(H * 2) + kc_chunk(f) * 16;
       }
       cstep = BK * 2;
-    } else if constexpr (MODE == G2F) {
-      cptr = (const char*)(p.w + (int64_t)d.e * H * I);
-      cbytes = (uint32_t)(H * I * 2);
+    } else if constexpr (MODE == G2F || DENSE) {
+      // weight rows [ncol][kdim]: down_proj[e] [H][I], or W_r [E][H]
+      const int ncol = DENSE ? p.E : H, kdim = DENSE ? H : I;
+      cptr = (const char*)(p.w + (int64_t)d.e * ncol * kdim);
+      cbytes = (uint32_t)(ncol * kdim * 2);
 #pragma unroll
       for (int i = 0; i < CPW; ++i) {
         const int f = kc_feature(wid + NW * i);
         const int wrow = d.ct * BC + f;
-        coff[i] = wrow < H ? (uint32_t)wrow * (uint32_t)(I * 2) + kc_chunk(f) * 16 : kOOB;
+        coff[i] = wrow < ncol ? (uint32_t)wrow * (uint32_t)(kdim * 2) + kc_chunk(f) * 16 : kOOB;
       }
       cstep = BK * 2;
     } else {
@@ -327,8 +338,8 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
         roff[i] = (uint32_t)tok * (uint32_t)(H * 2) + kc_chunk(f) * 16;
       }
       rstep = BK * 2;
-    } else if constexpr (TOKEN) {
-      const int ld = (MODE == G2F) ? I : (MODE == G2DX ? H : I2);
+    } else if constexpr (TOKEN || DENSE) {
+      const int ld = (MODE == G2F) ? I : ((MODE == G2DX || DENSE) ? H : I2);
       rptr = (const char*)(p.a0 + (int64_t)d.row0 * ld);
       rbytes = (uint32_t)((int64_t)(d.row_end - d.row0) * ld * 2);
 #pragma unroll
@@ -550,6 +561,28 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
 
     // --------------------------------------------------------- epilogue
     WAIT_VMCNT(0);    // no LDS DMA may still be landing in the stages
+    if constexpr (DENSE) {
+      if (p.out_f32) {
+        // fp32 logits: each lane stores its accumulators' 4 consecutive
+        // columns (16 bytes) directly; the output is T x E, small.
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+#pragma unroll
+          for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int r = cur.row0 + wr * WR + j * 32 + l32;
+              const int col = cur.ct * BC + wc * 128 + i * 32 + 8 * q + 4 * hl;
+              if (r < cur.row_end && col < p.E) {
+                const f32x4 v = {acc[i][j][4 * q + 0], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                                 acc[i][j][4 * q + 3]};
+                *(f32x4*)(p.out_f32 + (int64_t)r * p.E + col) = v;
+              }
+            }
+        __syncthreads();  // every wave is done reading the k-stages
+        continue;
+      }
+    }
     __syncthreads();  // every wave is done reading the k-stages
     bf16* stg = smem;  // [BR][SROW] bf16 staging tile
 #pragma unroll
@@ -668,6 +701,10 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       if constexpr (TOKEN) {
         nrows = cur.row_end;
         ld = H;
+        obase = p.out;
+      } else if constexpr (DENSE) {
+        nrows = cur.row_end;
+        ld = p.E;
         obase = p.out;
       } else {
         nrows = (MODE == G2DW) ? H : I2;
@@ -845,6 +882,37 @@ extern "C" int moe_amd_gemm_down(const void* act, const int32_t* offsets,
   a.out = (bf16*)y_out;
   a.S = S; a.E = E; a.H = H; a.I = I;
   return launch_token<G2F>(a, S, E, BC, H, tile_plan, (hipStream_t)stream);
+}
+
+extern "C" int moe_amd_router_linear(const void* hidden_states, const void* weight, int64_t T,
+                                     int E, int H, void* logits, int logits_dtype,
+                                     void* stream) {
+  const char* who = "router_linear";
+  MOE_REQUIRE(T >= 0 && E >= 1 && H > 0, MOE_ERR_ARG, "%s: bad sizes", who);
+  MOE_REQUIRE(H % 64 == 0 && E % 8 == 0, MOE_ERR_ARG,
+              "%s: H=%d must be a multiple of 64 and E=%d of 8", who, H, E);
+  MOE_REQUIRE(logits_dtype == MOE_DTYPE_BF16 || logits_dtype == MOE_DTYPE_F32, MOE_ERR_DTYPE,
+              "%s: logits dtype must be bf16 or fp32", who);
+  MOE_REQUIRE(hidden_states && weight && logits, MOE_ERR_ARG, "%s: null pointer", who);
+  MOE_ALIGNED(hidden_states, who);
+  MOE_ALIGNED(weight, who);
+  MOE_ALIGNED(logits, who);
+  // 32-bit byte offsets within one row tile and within the weight.
+  MOE_REQUIRE((int64_t)E * H * 2 < ((int64_t)1 << 31), MOE_ERR_UNSUPPORTED,
+              "%s: router weight too large", who);
+  if (T == 0) return MOE_OK;
+  GemmArgs a{};
+  a.w = (const bf16*)weight;
+  a.a0 = (const bf16*)hidden_states;
+  if (logits_dtype == MOE_DTYPE_F32) a.out_f32 = (float*)logits;
+  else a.out = (bf16*)logits;
+  a.T = T; a.E = E; a.H = H; a.I = 64;
+  a.n_ct = (E + BC - 1) / BC;
+  a.n_rt = (int)((T + 255) / 256);
+  const int64_t n_tiles = (int64_t)a.n_rt * a.n_ct;
+  MOE_REQUIRE(n_tiles < ((int64_t)1 << 30), MOE_ERR_UNSUPPORTED, "%s: too many tiles", who);
+  a.n_tiles = (int)n_tiles;
+  return launch<RL, 256>(a, a.n_tiles, (hipStream_t)stream);
 }
 
 extern "C" int moe_amd_gemm_down_backward_dx_dswiglu(const void* dy, const int32_t* offsets,

@@ -2,18 +2,18 @@
 
 ``moe_layer`` is the GPU form of Qwen3MoeSparseMoeBlock.forward
 (src/models/modeling_qwen3_moe.py:284-289) with either router: flatten to
-[T,H], gating linear (torch), HIP router kernel, HIP expert layer.
+[T,H], gating linear (MFMA kernel for bf16; ``gating="torch"`` keeps F.linear),
+HIP router kernel, HIP expert layer.
 ``SparseMoeBlock`` wraps it with the reference's parameter names
 (``gate.weight``, ``experts.gate_up_proj``, ``experts.down_proj``).
 """
 from __future__ import annotations
 
 import torch
-import torch.nn.functional as F
 from torch import nn
 
 from .experts import experts_forward
-from .router import SigmoidTopKFunction, SoftmaxTopKFunction
+from .router import SigmoidTopKFunction, SoftmaxTopKFunction, gating_linear
 
 
 def moe_layer(x: torch.Tensor, w_router: torch.Tensor, gate_up_proj: torch.Tensor,
@@ -21,13 +21,16 @@ def moe_layer(x: torch.Tensor, w_router: torch.Tensor, gate_up_proj: torch.Tenso
               renormalize: bool = True, logit_offset: torch.Tensor | None = None,
               expert_bias: torch.Tensor | None = None, scaling_factor: float | None = None,
               num_groups: int | None = None, group_topk: int | None = None,
-              tokens_per_expert: torch.Tensor | None = None):
+              tokens_per_expert: torch.Tensor | None = None, gating: str = "hip"):
     """Returns (out [T,H], router_logits [T,E] fp32, weights [T,K], index [T,K])."""
+    if gating not in ("hip", "torch"):
+        raise ValueError(f"unknown gating {gating!r}")
+    hip = gating == "hip"
     if router == "softmax":
-        logits = F.linear(x, w_router)
+        logits = gating_linear(x, w_router, fp32=False, hip=hip)
         probs, w, idx = SoftmaxTopKFunction.apply(logits, top_k, renormalize, logit_offset)
     elif router == "sigmoid":
-        logits = F.linear(x.float(), w_router.float())
+        logits = gating_linear(x, w_router, fp32=True, hip=hip)
         probs, w, idx = SigmoidTopKFunction.apply(logits, expert_bias, top_k, renormalize,
                                                   scaling_factor, num_groups, group_topk,
                                                   x.dtype, tokens_per_expert)

@@ -70,6 +70,25 @@ def _contig(t: torch.Tensor) -> torch.Tensor:
 
 # ----------------------------------------------------------------- router
 
+def router_linear(x: torch.Tensor, weight: torch.Tensor,
+                  out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """logits [T,E] = x [T,H] . weight [E,H]^T on MFMA (bf16 inputs, fp32
+    accumulation), returned in out_dtype (bf16 or fp32)."""
+    _need_cuda(x, weight)
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise TypeError("router_linear takes bf16 hidden states and weight")
+    x = _contig(x)
+    weight = _contig(weight)
+    T, H = x.shape
+    E = weight.shape[0]
+    if weight.shape[1] != H:
+        raise ValueError(f"router_linear: weight {tuple(weight.shape)} vs hidden {tuple(x.shape)}")
+    logits = torch.empty(T, E, device=x.device, dtype=out_dtype)
+    _call("moe_amd_router_linear", x.data_ptr(), weight.data_ptr(), T, E, H, logits.data_ptr(),
+          _dtype_code(out_dtype), _stream(x))
+    return logits
+
+
 def router_softmax_topk(logits: torch.Tensor, top_k: int, renormalize: bool = True,
                         logit_offset: torch.Tensor | None = None,
                         tokens_per_expert: torch.Tensor | None = None):

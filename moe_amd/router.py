@@ -3,9 +3,11 @@
 Both subclass transformers' ``Qwen3MoeTopKRouter`` so that HF's
 OutputRecorder keeps capturing index 0 of their output as router_logits
 (src/models/modeling_qwen3_moe.py:375-379; the reason the reference's
-DeepSeekRouter subclasses it, src/models/router.py:73-79).  The gating linear
-stays a torch ``F.linear`` so its logits are bit-identical to the reference's
-on the same device.
+DeepSeekRouter subclasses it, src/models/router.py:73-79).  By default their
+gating linear stays a torch ``F.linear``, so the logits are bit-identical to
+the reference's on the same device; ``hip_gating_linear = True`` switches it
+to the MFMA kernel (``gating_linear``), whose logits differ only in fp32
+summation order (and so can flip a top-k choice between near-tied experts).
 """
 from __future__ import annotations
 
@@ -28,6 +30,52 @@ except Exception:  # pragma: no cover - transformers absent: plain module base
             self.norm_topk_prob = config.norm_topk_prob
             self.hidden_dim = config.hidden_size
             self.weight = nn.Parameter(torch.zeros(self.num_experts, self.hidden_dim))
+
+
+class RouterLinearFunction(torch.autograd.Function):
+    """logits = x . W^T on the MFMA kernel (bf16 inputs, fp32 accumulation),
+    logits in bf16 (F.linear on bf16 tensors, src/models/modeling_qwen3_moe.py:
+    268-270) or fp32 (F.linear(h.float(), W.float()), src/models/router.py:
+    107-109).  The backward is the matching torch linear backward: in bf16
+    for bf16 logits, in fp32 (then cast to the inputs' dtypes) for fp32."""
+
+    @staticmethod
+    def forward(ctx, x, weight, out_dtype):
+        ctx.save_for_backward(x, weight)
+        ctx.out_dtype = out_dtype
+        return ops.router_linear(x, weight, out_dtype)
+
+    @staticmethod
+    def backward(ctx, d_logits):
+        x, weight = ctx.saved_tensors
+        dx = dw = None
+        if ctx.out_dtype == torch.float32:
+            g = d_logits.float()
+            if ctx.needs_input_grad[0]:
+                dx = (g @ weight.float()).to(x.dtype)
+            if ctx.needs_input_grad[1]:
+                dw = (g.t().contiguous() @ x.float()).to(weight.dtype)
+        else:
+            g = d_logits.to(x.dtype)
+            if ctx.needs_input_grad[0]:
+                dx = g @ weight
+            if ctx.needs_input_grad[1]:
+                dw = g.t().contiguous() @ x
+        return dx, dw, None
+
+
+def gating_linear(x: torch.Tensor, weight: torch.Tensor, fp32: bool, hip: bool = True):
+    """The router's gating linear: bf16 logits (softmax router) or fp32 logits
+    (DeepSeek router).  Runs on the MFMA kernel when ``hip`` and both operands
+    are bf16 on the GPU (H a multiple of 64, E of 8); otherwise torch's F.linear
+    on the same device."""
+    E, H = weight.shape
+    if (hip and x.is_cuda and x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16
+            and H % 64 == 0 and E % 8 == 0):
+        return RouterLinearFunction.apply(x, weight, torch.float32 if fp32 else torch.bfloat16)
+    if fp32:
+        return F.linear(x.float(), weight.float())
+    return F.linear(x, weight)
 
 
 class SoftmaxTopKFunction(torch.autograd.Function):
@@ -86,13 +134,15 @@ class MI355XTopKRouter(_RouterBase):
     ``logit_offset`` (optional [E] fp32 attribute) is added to the logits
     before the softmax; the skewed-routing benchmark config uses it."""
 
+    hip_gating_linear = False  # True: MFMA gating linear (see module docstring)
+
     def __init__(self, config):
         super().__init__(config)
         self.logit_offset: torch.Tensor | None = None
 
     def forward(self, hidden_states):
         hidden_states = hidden_states.reshape(-1, self.hidden_dim)
-        logits = F.linear(hidden_states, self.weight)
+        logits = gating_linear(hidden_states, self.weight, fp32=False, hip=self.hip_gating_linear)
         return SoftmaxTopKFunction.apply(logits, self.top_k, bool(self.norm_topk_prob),
                                          self.logit_offset)
 
@@ -124,9 +174,11 @@ class MI355XDeepSeekRouter(_RouterBase):
                              torch.zeros(self.num_experts, dtype=torch.float32), persistent=False)
         self._last_top_k_idx = None
 
+    hip_gating_linear = False  # True: MFMA gating linear with fp32 logits
+
     def forward(self, hidden_states):
         hidden_states = hidden_states.reshape(-1, self.hidden_dim)
-        logits = F.linear(hidden_states.float(), self.weight.float())
+        logits = gating_linear(hidden_states, self.weight, fp32=True, hip=self.hip_gating_linear)
         counting = torch.is_grad_enabled()
         scores, w, idx = SigmoidTopKFunction.apply(
             logits, self.expert_bias, self.top_k, bool(self.norm_topk_prob), self.scaling_factor,

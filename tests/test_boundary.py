@@ -180,7 +180,7 @@ def test_shared_bank_accumulates_gradients_across_layers():
     w1d = w1.cuda().requires_grad_(True)
     w2d = w2.cuda().requires_grad_(True)
     for layer in range(2):
-        out, _, _, _ = moe_layer(x.cuda(), r[layer].cuda(), w1d, w2d, K)
+        out, _, _, _ = moe_layer(x.cuda(), r[layer].cuda(), w1d, w2d, K, gating="torch")
         out.backward(d[layer].cuda())
     torch.cuda.synchronize()
     acc1 = torch.zeros(E, 2 * I, H, dtype=torch.float64)

@@ -155,3 +155,42 @@ def test_sigmoid_router_backward_parity():
     (gl,) = torch.autograd.grad((w * dw).sum() + (scores * ds).sum(), logits)
     ref = O.sigmoid_router_backward(scores.detach().cpu(), idx.cpu(), dw.cpu(), ds.cpu(), True, 2.5)
     assert torch.allclose(gl.cpu(), ref, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("T,H,E", [
+    (65536, 2048, 128),   # L router GEMM
+    (4096, 2048, 1792),   # retrofit expert count (token sample)
+    (2048, 1024, 16),     # XS expert count
+    (1001, 128, 8),       # ragged T, one column tile mostly empty
+    (256, 64, 264),       # E just past one 256-column tile
+])
+def test_router_linear_parity(T, H, E):
+    """The MFMA gating linear against fp32 torch on the same bf16 inputs: the
+    fp32 output within 1e-5 of max|logit| (products of bf16 values are exact in
+    fp32, only the summation order differs), the bf16 output within one bf16
+    rounding of the fp32 result."""
+    print(f"router linear T={T} H={H} E={E}", flush=True)
+    g = torch.Generator().manual_seed(T + E + H)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(DEV)
+    wr = (torch.randn(E, H, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    ref = x.float() @ wr.float().t()
+    out32 = ops.router_linear(x, wr, torch.float32)
+    out16 = ops.router_linear(x, wr, torch.bfloat16)
+    torch.cuda.synchronize()
+    assert out32.dtype == torch.float32 and out16.dtype == torch.bfloat16
+    assert _rel(out32, ref) < 1e-5
+    # bf16: |out16 - ref| <= half an ulp of bf16 at the value plus the fp32 noise
+    err = (out16.double() - ref.double()).abs()
+    bound = ref.double().abs() * 2.0 ** -8 + 1e-5 * ref.abs().max().item()
+    assert bool((err <= bound).all())
+
+
+def test_router_linear_rejects():
+    x = torch.zeros(64, 96, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(RuntimeError, match="multiple of 64"):
+        ops.router_linear(x, torch.zeros(8, 96, dtype=torch.bfloat16, device=DEV))
+    x = torch.zeros(64, 128, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(RuntimeError, match="of 8"):
+        ops.router_linear(x, torch.zeros(12, 128, dtype=torch.bfloat16, device=DEV))
+    with pytest.raises(TypeError):
+        ops.router_linear(x.float(), torch.zeros(8, 128, device=DEV))
