@@ -1,10 +1,11 @@
 """Benchmark: MoE layer forward+backward on one MI355X.
 
 A step is one forward+backward of the whole expert layer over one batch of
-synthetic inputs already resident in HBM: gating linear (torch) -> HIP router
--> HIP permutation -> grouped GEMM-1 + SwiGLU -> grouped GEMM-2 -> combine,
-then the full backward (combine, GEMM-2 dX+dSwiGLU, GEMM-2 dW, GEMM-1 dX,
-GEMM-1 dW, gather, router backward, gating-linear backward).  Default
+synthetic inputs already resident in HBM: gating linear (MFMA) -> router
+softmax/top-k -> permutation -> grouped GEMM-1 + SwiGLU -> grouped GEMM-2 ->
+combine, then the full backward (combine, GEMM-2 dW, GEMM-2 dX+dSwiGLU,
+GEMM-1 dW, router backward, gating-linear dW (split-K), GEMM-1 dX, gating-
+linear dX, gather + add), every kernel hand-written HIP.  Default
 workload: the L (Qwen3-30B-A3B) layer, T=65536, H=2048, E=128, K=8, I=768,
 bf16.
 
@@ -99,20 +100,23 @@ def copy_calibration(nbytes: int) -> None:
     print(json.dumps({"copy_calibration_bytes": nbytes, "launches": 3}), flush=True)
 
 
-def recorded_traffic(kernel: str):
-    """HBM bytes per launch of `kernel` as measured by rocprofv3 FETCH_SIZE and
-    WRITE_SIZE counters (scaled by the copy calibration) and recorded in
-    profiles/gemm_hbm_traffic_L.md as `traffic_bytes_per_launch[<kernel>] = N`."""
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                        "gemm_hbm_traffic_L.md")
-    try:
-        for line in open(path):
-            line = line.strip().strip("`")
-            if line.startswith(f"traffic_bytes_per_launch[{kernel}]"):
-                return float(line.split("=", 1)[1])
-    except OSError:
-        pass
-    return None
+# HBM bytes per launch of the six grouped GEMMs at the L shape, measured with
+# rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE (one pass each) and scaled by
+# the same counters on a plain copy of known size (`--copy-calibration`); the
+# commands and per-counter figures are in profiles/gemm_hbm_traffic_L.md.
+RECORDED_TRAFFIC_L = {
+    "gemm_gate_up_swiglu": 12051779536,
+    "gemm_down": 5349018615,
+    "gemm_down_backward_dx_dswiglu": 7894323164,
+    "gemm_gate_up_backward_dx": 8422120319,
+    "gemm_down_backward_dw": 4212811645,
+    "gemm_gate_up_backward_dw": 12081383239,
+}
+
+
+def recorded_traffic(cfg_name: str, kernel: str):
+    """Measured HBM bytes per launch of `kernel` (L shape only), else None."""
+    return RECORDED_TRAFFIC_L.get(kernel) if cfg_name.startswith("L") else None
 
 
 def main():
@@ -227,7 +231,7 @@ def main():
         "roofline": {"bound": "mfma", "kernel": dom.replace("moe_amd_", ""),
                      "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": recorded_traffic(dom.replace("moe_amd_", ""))},
+                     "traffic": recorded_traffic(cfg.name, dom.replace("moe_amd_", ""))},
         "kernels": kernels,
     }
     if not args.no_cpu_baseline:

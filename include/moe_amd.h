@@ -66,6 +66,24 @@ const char* moe_amd_last_error(void);
 int moe_amd_router_linear(const void* hidden_states, const void* weight, int64_t T, int E, int H,
                           void* logits, int logits_dtype, void* stream);
 
+/* The gating linear's input gradient for bf16 logits: d_x[T,H] =
+ * bf16(d_logits[T,E] . weight[E,H]) (bf16 inputs, fp32 accumulation) -- the
+ * grad_input of F.linear's backward (autograd of
+ * src/models/modeling_qwen3_moe.py:268-270).  H multiple of 256, E of 8. */
+int moe_amd_router_linear_backward_dx(const void* d_logits, const void* weight, int64_t T, int E,
+                                      int H, void* d_x, void* stream);
+
+/* The gating linear's weight gradient for bf16 logits: d_weight[E,H] =
+ * bf16(sum_t d_logits[t,:]^T hidden_states[t,:]), the grad_weight of
+ * F.linear's backward.  Split over token chunks (one fp32 partial per chunk
+ * in the caller's workspace, moe_amd_router_linear_backward_dw_workspace_size
+ * bytes), reduced in chunk order: deterministic.  H multiple of 256; E a
+ * multiple of 8, at most 256. */
+size_t moe_amd_router_linear_backward_dw_workspace_size(int64_t T, int E, int H);
+int moe_amd_router_linear_backward_dw(const void* d_logits, const void* hidden_states, int64_t T,
+                                      int E, int H, void* workspace, size_t workspace_bytes,
+                                      void* d_weight, void* stream);
+
 /* Softmax router after the gating linear: probs = softmax(float(logits) +
  * logit_offset) over E, top-K (value descending, lower expert id first on
  * equal values), optional renormalisation by the top-K sum (no epsilon).
@@ -205,6 +223,16 @@ int moe_amd_combine_backward(const void* d_out, const void* y, const int32_t* sl
  * d_x[t] = sum_k d_xs[slot[t*K+k]] (fp32 accumulation, sentinels skipped). */
 int moe_amd_gather_backward(const void* d_xs, const int32_t* slot, const int32_t* offsets,
                             int64_t T, int K, int E, int H, int dtype, void* d_x, void* stream);
+
+/* The same plus a second gradient of the hidden states (the gating linear's,
+ * when router and experts are one autograd node): d_x[t] =
+ * dtype(dtype(sum_k d_xs[slot[t*K+k]]) + addend[t]), the rounding of
+ * autograd accumulating two dtype-typed gradients of hidden_states.  No
+ * counterpart in the reference, which adds the two gradients with a separate
+ * elementwise kernel.  addend [T,H] in dtype. */
+int moe_amd_gather_backward_add(const void* d_xs, const int32_t* slot, const int32_t* offsets,
+                                const void* addend, int64_t T, int K, int E, int H, int dtype,
+                                void* d_x, void* stream);
 
 #ifdef __cplusplus
 }

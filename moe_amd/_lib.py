@@ -37,6 +37,9 @@ SIGNATURES: dict[str, tuple] = {
     "moe_amd_abi_version": (_i, []),
     "moe_amd_last_error": (ctypes.c_char_p, []),
     "moe_amd_router_linear": (_i, [_p, _p, _i64, _i, _i, _p, _i, _p]),
+    "moe_amd_router_linear_backward_dx": (_i, [_p, _p, _i64, _i, _i, _p, _p]),
+    "moe_amd_router_linear_backward_dw_workspace_size": (_sz, [_i64, _i, _i]),
+    "moe_amd_router_linear_backward_dw": (_i, [_p, _p, _i64, _i, _i, _p, _sz, _p, _p]),
     "moe_amd_router_softmax_topk": (_i, [_p, _i, _p, _i64, _i, _i, _i, _p, _p, _p, _p, _p]),
     "moe_amd_router_softmax_topk_backward": (_i, [_p, _p, _p, _p, _i64, _i, _i, _i, _p, _i, _p]),
     "moe_amd_router_sigmoid_topk": (
@@ -59,6 +62,7 @@ SIGNATURES: dict[str, tuple] = {
     "moe_amd_combine_backward": (
         _i, [_p, _p, _p, _p, _p, _i, _i64, _i, _i, _i, _i, _p, _p, _p]),
     "moe_amd_gather_backward": (_i, [_p, _p, _p, _i64, _i, _i, _i, _i, _p, _p]),
+    "moe_amd_gather_backward_add": (_i, [_p, _p, _p, _p, _i64, _i, _i, _i, _i, _p, _p]),
 }
 
 _lock = threading.Lock()

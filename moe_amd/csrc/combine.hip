@@ -25,6 +25,7 @@ template <> struct Vec<bf16> {
     for (int i = 0; i < 4; ++i) w[i] = pack_bf2(v[2 * i], v[2 * i + 1]);
     *(u32x4*)p = w;
   }
+  __device__ static float round(float v) { return round_bf(v); }
 };
 template <> struct Vec<float> {
   static constexpr int N = 4;
@@ -37,6 +38,7 @@ template <> struct Vec<float> {
     f32x4 w = {v[0], v[1], v[2], v[3]};
     *(f32x4*)p = w;
   }
+  __device__ static float round(float v) { return v; }
 };
 
 __device__ __forceinline__ float load_w(const void* w, int wdt, int64_t i) {
@@ -118,7 +120,7 @@ __global__ __launch_bounds__(64 * kWaves) void combine_bwd_kernel(
 template <typename T>
 __global__ __launch_bounds__(64 * kWaves) void gather_bwd_kernel(
     const T* __restrict__ dxs, const int* __restrict__ slot, const int* __restrict__ offsets,
-    int64_t ntok, int K, int E, int H, T* __restrict__ dx) {
+    const T* __restrict__ addend, int64_t ntok, int K, int E, int H, T* __restrict__ dx) {
   constexpr int N = Vec<T>::N;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int nvalid = offsets[E];
@@ -135,6 +137,14 @@ __global__ __launch_bounds__(64 * kWaves) void gather_bwd_kernel(
         Vec<T>::load(dxs + (int64_t)s * H + h0, v);
 #pragma unroll
         for (int i = 0; i < N; ++i) acc[i] += v[i];
+      }
+      if (addend) {
+        // a second gradient of the same tensor: round the sum to T first, as
+        // autograd's accumulation of two T-typed gradients does
+        float a[N];
+        Vec<T>::load(addend + t * H + h0, a);
+#pragma unroll
+        for (int i = 0; i < N; ++i) acc[i] = Vec<T>::round(acc[i]) + a[i];
       }
       Vec<T>::store(dx + t * H + h0, acc);
     }
@@ -212,22 +222,38 @@ extern "C" int moe_amd_combine_backward(const void* d_out, const void* y, const 
   return check_launch(who);
 }
 
-extern "C" int moe_amd_gather_backward(const void* d_xs, const int32_t* slot,
-                                       const int32_t* offsets, int64_t T, int K, int E, int H,
-                                       int dtype, void* d_x, void* stream) {
-  const char* who = "gather_backward";
+int gather_backward_impl(const void* d_xs, const int32_t* slot, const int32_t* offsets,
+                         const void* addend, int64_t T, int K, int E, int H, int dtype, void* d_x,
+                         void* stream, const char* who) {
   int rc = check_rows(T, K, E, H, dtype, who);
   if (rc) return rc;
   MOE_REQUIRE(offsets && d_x && (T == 0 || (d_xs && slot)), MOE_ERR_ARG, "%s: null pointer",
               who);
-  MOE_REQUIRE(al16(d_x) && (T == 0 || al16(d_xs)), MOE_ERR_ALIGN, "%s: misaligned pointer", who);
+  MOE_REQUIRE(al16(d_x) && (T == 0 || al16(d_xs)) && (!addend || al16(addend)), MOE_ERR_ALIGN,
+              "%s: misaligned pointer", who);
   if (T == 0) return MOE_OK;
   hipStream_t st = (hipStream_t)stream;
   if (dtype == MOE_DTYPE_BF16)
     gather_bwd_kernel<bf16><<<grid_tokens(T), 64 * kWaves, 0, st>>>(
-        (const bf16*)d_xs, slot, offsets, T, K, E, H, (bf16*)d_x);
+        (const bf16*)d_xs, slot, offsets, (const bf16*)addend, T, K, E, H, (bf16*)d_x);
   else
     gather_bwd_kernel<float><<<grid_tokens(T), 64 * kWaves, 0, st>>>(
-        (const float*)d_xs, slot, offsets, T, K, E, H, (float*)d_x);
+        (const float*)d_xs, slot, offsets, (const float*)addend, T, K, E, H, (float*)d_x);
   return check_launch(who);
+}
+
+extern "C" int moe_amd_gather_backward(const void* d_xs, const int32_t* slot,
+                                       const int32_t* offsets, int64_t T, int K, int E, int H,
+                                       int dtype, void* d_x, void* stream) {
+  return gather_backward_impl(d_xs, slot, offsets, nullptr, T, K, E, H, dtype, d_x, stream,
+                              "gather_backward");
+}
+
+extern "C" int moe_amd_gather_backward_add(const void* d_xs, const int32_t* slot,
+                                           const int32_t* offsets, const void* addend, int64_t T,
+                                           int K, int E, int H, int dtype, void* d_x,
+                                           void* stream) {
+  MOE_REQUIRE(addend, MOE_ERR_ARG, "gather_backward_add: null addend");
+  return gather_backward_impl(d_xs, slot, offsets, addend, T, K, E, H, dtype, d_x, stream,
+                              "gather_backward_add");
 }

@@ -70,7 +70,10 @@ constexpr int kWaves = 4;
 constexpr int SROW = 260;  // bf16 per row of the epilogue staging tile (520 B: conflict-free)
 
 // RL: the router's dense linear, logits[T, E] = x[T, H] . W_r[E, H]^T.
-enum Mode { G1F = 0, G2F = 1, G2DX = 2, G1DX = 3, G2DW = 4, G1DW = 5, RL = 6 };
+// RDX: its input gradient, d_x[T, H] = d_logits[T, E] . W_r[E, H].
+// RDW: its weight gradient split over token chunks c (split-K), fp32
+//      partial[c][E][H] = sum_{t in chunk c} d_logits[t, :]^T x[t, :].
+enum Mode { G1F = 0, G2F = 1, G2DX = 2, G1DX = 3, G2DW = 4, G1DW = 5, RL = 6, RDX = 7, RDW = 8 };
 
 struct GemmArgs {
   const bf16* x;         // hidden_states [T,H]
@@ -83,7 +86,8 @@ struct GemmArgs {
   const int4* tile_info; // token modes: {expert, first row, end row, 0} per row tile
   bf16* out;
   bf16* out2;            // gate_up output of G1F (may be null)
-  float* out_f32;        // RL: fp32 logits (null: bf16 logits in out)
+  float* out_f32;        // RL: fp32 logits (null: bf16 logits in out); RDW: fp32 partials
+  int chunk_rows;        // RDW: tokens per split-K chunk
   int64_t T, S;
   int E, H, I, topk;
   uint32_t tok_mul;      // n / topk == (n * tok_mul) >> tok_shift for 0 <= n < 2^31
@@ -165,8 +169,8 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
   constexpr int NW = kWaves<BR>;                          // waves, as NW/2 rows x 2 columns
   constexpr int NTHR = NW * 64;
   constexpr bool TOKEN = MODE <= G1DX;                    // rows = routed rows of one expert
-  constexpr bool DENSE = MODE == RL;                      // rows = all T tokens, one "expert"
-  constexpr bool COL_KM = !(MODE == G1F || MODE == G2F || DENSE);  // column operand k-major
+  constexpr bool DENSE = MODE == RL || MODE == RDX;       // rows = all T tokens, one "expert"
+  constexpr bool COL_KM = !(MODE == G1F || MODE == G2F || MODE == RL);  // column operand k-major
   constexpr bool ROW_KM = !TOKEN && !DENSE;               // row operand k-major (dW)
   constexpr int WR = BR / (NW / 2);                       // rows per wave
   constexpr int TJ = WR / 32;                             // MFMA row sub-tiles per wave
@@ -221,8 +225,13 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       d.ct = rem - rt * p.n_ct;
       d.row0 = rt * BR;
       d.row_end = 0;
-      d.kbeg = p.offsets[d.e];
-      d.kend = p.offsets[d.e + 1];
+      if constexpr (MODE == RDW) {
+        d.kbeg = (int)min((int64_t)d.e * p.chunk_rows, p.T);
+        d.kend = (int)min((int64_t)d.kbeg + p.chunk_rows, p.T);
+      } else {
+        d.kbeg = p.offsets[d.e];
+        d.kend = p.offsets[d.e + 1];
+      }
     }
     // Tile fields are wave-uniform; say so, so that the buffer descriptors
     // built from them stay in SGPRs.
@@ -233,7 +242,8 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
     d.kbeg = __builtin_amdgcn_readfirstlane(d.kbeg);
     d.kend = __builtin_amdgcn_readfirstlane(d.kend);
     int K_len;
-    if constexpr (MODE == G1F || MODE == G2DX || DENSE) K_len = H;
+    if constexpr (MODE == G1F || MODE == G2DX || MODE == RL) K_len = H;
+    else if constexpr (MODE == RDX) K_len = p.E;
     else if constexpr (MODE == G2F) K_len = I;
     else if constexpr (MODE == G1DX) K_len = I2;
     else K_len = d.kend - d.kbeg;
@@ -286,9 +296,9 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
         coff[i] = (uint32_t)wrow * (uint32_t)(H * 2) + kc_chunk(f) * 16;
       }
       cstep = BK * 2;
-    } else if constexpr (MODE == G2F || DENSE) {
+    } else if constexpr (MODE == G2F || MODE == RL) {
       // weight rows [ncol][kdim]: down_proj[e] [H][I], or W_r [E][H]
-      const int ncol = DENSE ? p.E : H, kdim = DENSE ? H : I;
+      const int ncol = MODE == RL ? p.E : H, kdim = MODE == RL ? H : I;
       cptr = (const char*)(p.w + (int64_t)d.e * ncol * kdim);
       cbytes = (uint32_t)(ncol * kdim * 2);
 #pragma unroll
@@ -305,6 +315,10 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
         cptr = (const char*)(p.w + (int64_t)d.e * H * I);
         cbytes = (uint32_t)(H * I * 2);
         ld = I;
+      } else if constexpr (MODE == RDX) {  // W_r [E][H]: k = expert, features = H
+        cptr = (const char*)p.w;
+        cbytes = (uint32_t)(p.E * H * 2);
+        ld = H;
       } else if constexpr (MODE == G1DX) {
         cptr = (const char*)(p.w + (int64_t)d.e * I2 * H);
         cbytes = (uint32_t)(I2 * H * 2);
@@ -313,6 +327,10 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
         cptr = (const char*)(p.a1 + (int64_t)d.kbeg * I);
         cbytes = (uint32_t)((int64_t)(d.kend - d.kbeg) * I * 2);
         ld = I;
+      } else if constexpr (MODE == RDW) {  // hidden_states rows of the chunk
+        cptr = (const char*)(p.x + (int64_t)d.kbeg * H);
+        cbytes = (uint32_t)((int64_t)(d.kend - d.kbeg) * H * 2);
+        ld = H;
       } else {  // G1DW: rows of hidden_states gathered through row_src
         cptr = (const char*)p.x;
         cbytes = (uint32_t)(p.T * H * 2);
@@ -339,7 +357,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       }
       rstep = BK * 2;
     } else if constexpr (TOKEN || DENSE) {
-      const int ld = (MODE == G2F) ? I : ((MODE == G2DX || DENSE) ? H : I2);
+      const int ld = (MODE == G2F) ? I : ((MODE == G2DX || MODE == RL) ? H : (MODE == RDX ? p.E : I2));
       rptr = (const char*)(p.a0 + (int64_t)d.row0 * ld);
       rbytes = (uint32_t)((int64_t)(d.row_end - d.row0) * ld * 2);
 #pragma unroll
@@ -350,7 +368,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       }
       rstep = BK * 2;
     } else {
-      const int ld = (MODE == G2DW) ? H : I2;
+      const int ld = (MODE == G2DW) ? H : (MODE == RDW ? p.E : I2);
       rptr = (const char*)(p.a0 + (int64_t)d.kbeg * ld);
       rbytes = (uint32_t)((int64_t)(d.kend - d.kbeg) * ld * 2);
 #pragma unroll
@@ -561,10 +579,14 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
 
     // --------------------------------------------------------- epilogue
     WAIT_VMCNT(0);    // no LDS DMA may still be landing in the stages
-    if constexpr (DENSE) {
+    if constexpr (MODE == RL || MODE == RDW) {
       if (p.out_f32) {
-        // fp32 logits: each lane stores its accumulators' 4 consecutive
-        // columns (16 bytes) directly; the output is T x E, small.
+        // fp32 output (RL's logits, RDW's partials): each lane stores its
+        // accumulators' 4 consecutive columns (16 bytes) directly; these
+        // outputs are small (T x E, chunks x E x H).
+        const int nrows = MODE == RL ? cur.row_end : p.E;
+        const int ld = MODE == RL ? p.E : H;
+        float* const ob = MODE == RL ? p.out_f32 : p.out_f32 + (int64_t)cur.e * p.E * H;
 #pragma unroll
         for (int j = 0; j < TJ; ++j)
 #pragma unroll
@@ -573,10 +595,10 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
             for (int q = 0; q < 4; ++q) {
               const int r = cur.row0 + wr * WR + j * 32 + l32;
               const int col = cur.ct * BC + wc * 128 + i * 32 + 8 * q + 4 * hl;
-              if (r < cur.row_end && col < p.E) {
+              if (r < nrows && col < ld) {
                 const f32x4 v = {acc[i][j][4 * q + 0], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
                                  acc[i][j][4 * q + 3]};
-                *(f32x4*)(p.out_f32 + (int64_t)r * p.E + col) = v;
+                *(f32x4*)(ob + (int64_t)r * ld + col) = v;
               }
             }
         __syncthreads();  // every wave is done reading the k-stages
@@ -704,7 +726,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
         obase = p.out;
       } else if constexpr (DENSE) {
         nrows = cur.row_end;
-        ld = p.E;
+        ld = MODE == RL ? p.E : H;
         obase = p.out;
       } else {
         nrows = (MODE == G2DW) ? H : I2;
@@ -893,7 +915,8 @@ extern "C" int moe_amd_router_linear(const void* hidden_states, const void* weig
               "%s: H=%d must be a multiple of 64 and E=%d of 8", who, H, E);
   MOE_REQUIRE(logits_dtype == MOE_DTYPE_BF16 || logits_dtype == MOE_DTYPE_F32, MOE_ERR_DTYPE,
               "%s: logits dtype must be bf16 or fp32", who);
-  MOE_REQUIRE(hidden_states && weight && logits, MOE_ERR_ARG, "%s: null pointer", who);
+  MOE_REQUIRE(weight && (T == 0 || (hidden_states && logits)), MOE_ERR_ARG,
+              "%s: null pointer", who);
   MOE_ALIGNED(hidden_states, who);
   MOE_ALIGNED(weight, who);
   MOE_ALIGNED(logits, who);
@@ -913,6 +936,105 @@ extern "C" int moe_amd_router_linear(const void* hidden_states, const void* weig
   MOE_REQUIRE(n_tiles < ((int64_t)1 << 30), MOE_ERR_UNSUPPORTED, "%s: too many tiles", who);
   a.n_tiles = (int)n_tiles;
   return launch<RL, 256>(a, a.n_tiles, (hipStream_t)stream);
+}
+
+extern "C" int moe_amd_router_linear_backward_dx(const void* d_logits, const void* weight,
+                                                 int64_t T, int E, int H, void* d_x,
+                                                 void* stream) {
+  const char* who = "router_linear_backward_dx";
+  MOE_REQUIRE(T >= 0 && E >= 1 && H > 0, MOE_ERR_ARG, "%s: bad sizes", who);
+  MOE_REQUIRE(H % 256 == 0 && E % 8 == 0, MOE_ERR_ARG,
+              "%s: H=%d must be a multiple of 256 and E=%d of 8", who, H, E);
+  MOE_REQUIRE(weight && (T == 0 || (d_logits && d_x)), MOE_ERR_ARG, "%s: null pointer", who);
+  MOE_ALIGNED(d_logits, who);
+  MOE_ALIGNED(weight, who);
+  MOE_ALIGNED(d_x, who);
+  MOE_REQUIRE((int64_t)E * H * 2 < ((int64_t)1 << 31), MOE_ERR_UNSUPPORTED,
+              "%s: router weight too large", who);
+  if (T == 0) return MOE_OK;
+  GemmArgs a{};
+  a.w = (const bf16*)weight;
+  a.a0 = (const bf16*)d_logits;
+  a.out = (bf16*)d_x;
+  a.T = T; a.E = E; a.H = H; a.I = 64;
+  a.n_ct = H / BC;
+  a.n_rt = (int)((T + 255) / 256);
+  const int64_t n_tiles = (int64_t)a.n_rt * a.n_ct;
+  MOE_REQUIRE(n_tiles < ((int64_t)1 << 30), MOE_ERR_UNSUPPORTED, "%s: too many tiles", who);
+  a.n_tiles = (int)n_tiles;
+  return launch<RDX, 256>(a, a.n_tiles, (hipStream_t)stream);
+}
+
+// Split-K reduction of RDW: d_w[e][h] = bf16(sum_c partial[c][e][h]), fp32
+// sums in chunk order (deterministic); 4 elements per thread (n % 4 == 0).
+// With no chunks it writes zeros.
+__global__ void reduce_chunks_kernel(const float* __restrict__ part, int nchunk, int64_t n,
+                                     bf16* __restrict__ out) {
+  const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (i >= n) return;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int c = 0; c < nchunk; ++c) acc += *(const f32x4*)(part + (int64_t)c * n + i);
+  u32x2 w = {pack_bf2(acc[0], acc[1]), pack_bf2(acc[2], acc[3])};
+  *(u32x2*)(out + i) = w;
+}
+
+int rdw_chunks(int64_t T, int H) {
+  // about one workgroup per CU: chunks x (H / 256) column tiles
+  int c = num_cus() / (H / BC);
+  if (c < 1) c = 1;
+  const int64_t max_c = (T + 63) / 64;  // at least 64 tokens per chunk
+  if (c > max_c) c = (int)max_c;
+  return c < 1 ? 1 : c;
+}
+
+extern "C" size_t moe_amd_router_linear_backward_dw_workspace_size(int64_t T, int E, int H) {
+  if (T <= 0 || E <= 0 || H < BC) return 0;
+  return (size_t)rdw_chunks(T, H) * (size_t)E * (size_t)H * sizeof(float);
+}
+
+extern "C" int moe_amd_router_linear_backward_dw(const void* d_logits, const void* hidden_states,
+                                                 int64_t T, int E, int H, void* workspace,
+                                                 size_t workspace_bytes, void* d_weight,
+                                                 void* stream) {
+  const char* who = "router_linear_backward_dw";
+  MOE_REQUIRE(T >= 0 && E >= 1 && H > 0, MOE_ERR_ARG, "%s: bad sizes", who);
+  MOE_REQUIRE(H % 256 == 0 && E % 8 == 0 && E <= 256, MOE_ERR_ARG,
+              "%s: H=%d must be a multiple of 256 and E=%d of 8, at most 256", who, H, E);
+  MOE_REQUIRE(d_weight && (T == 0 || (d_logits && hidden_states)), MOE_ERR_ARG,
+              "%s: null pointer", who);
+  MOE_ALIGNED(d_logits, who);
+  MOE_ALIGNED(hidden_states, who);
+  MOE_ALIGNED(d_weight, who);
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t n = (int64_t)E * H;
+  if (T == 0) {  // no tokens: a zero gradient (a fill kernel, safe under graph capture)
+    reduce_chunks_kernel<<<(unsigned)((n / 4 + 255) / 256), 256, 0, st>>>(nullptr, 0, n,
+                                                                         (bf16*)d_weight);
+    return check_launch(who);
+  }
+  const size_t need = moe_amd_router_linear_backward_dw_workspace_size(T, E, H);
+  MOE_REQUIRE(workspace && workspace_bytes >= need, MOE_ERR_WORKSPACE,
+              "%s: workspace of %zu bytes needed", who, need);
+  MOE_ALIGNED(workspace, who);
+  const int nchunk = rdw_chunks(T, H);
+  const int64_t chunk_rows = (T + nchunk - 1) / nchunk;
+  // chunk byte extents and the d_logits/x offsets stay below 2^31
+  MOE_REQUIRE(chunk_rows * (int64_t)H * 2 < ((int64_t)1 << 31), MOE_ERR_UNSUPPORTED,
+              "%s: token chunk too large", who);
+  GemmArgs a{};
+  a.a0 = (const bf16*)d_logits;
+  a.x = (const bf16*)hidden_states;
+  a.out_f32 = (float*)workspace;
+  a.T = T; a.E = E; a.H = H; a.I = 64;
+  a.chunk_rows = (int)chunk_rows;
+  a.n_rt = 1;
+  a.n_ct = H / BC;
+  a.n_tiles = nchunk * a.n_ct;
+  int rc = launch<RDW, 256>(a, a.n_tiles, st);
+  if (rc) return rc;
+  reduce_chunks_kernel<<<(unsigned)((n / 4 + 255) / 256), 256, 0, st>>>(
+      (const float*)workspace, nchunk, n, (bf16*)d_weight);
+  return check_launch(who);
 }
 
 extern "C" int moe_amd_gemm_down_backward_dx_dswiglu(const void* dy, const int32_t* offsets,

@@ -89,6 +89,40 @@ def router_linear(x: torch.Tensor, weight: torch.Tensor,
     return logits
 
 
+def router_linear_backward_dx(d_logits: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """d_x [T,H] = bf16(d_logits [T,E] . weight [E,H]) on MFMA (bf16 inputs)."""
+    _need_cuda(d_logits, weight)
+    if d_logits.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise TypeError("router_linear_backward_dx takes bf16 d_logits and weight")
+    d_logits = _contig(d_logits)
+    weight = _contig(weight)
+    T, E = d_logits.shape
+    H = weight.shape[1]
+    d_x = torch.empty(T, H, device=d_logits.device, dtype=torch.bfloat16)
+    _call("moe_amd_router_linear_backward_dx", d_logits.data_ptr(), weight.data_ptr(), T, E, H,
+          d_x.data_ptr(), _stream(d_logits))
+    return d_x
+
+
+def router_linear_backward_dw(d_logits: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+    """d_weight [E,H] = bf16(d_logits [T,E]^T . x [T,H]) on MFMA, split over
+    token chunks with fp32 partials (E <= 256)."""
+    _need_cuda(d_logits, x)
+    if d_logits.dtype != torch.bfloat16 or x.dtype != torch.bfloat16:
+        raise TypeError("router_linear_backward_dw takes bf16 d_logits and hidden states")
+    d_logits = _contig(d_logits)
+    x = _contig(x)
+    T, E = d_logits.shape
+    H = x.shape[1]
+    lib = _lib.load()
+    nbytes = lib.moe_amd_router_linear_backward_dw_workspace_size(T, E, H)
+    ws = torch.empty(max(nbytes, 16), device=x.device, dtype=torch.uint8)
+    d_w = torch.empty(E, H, device=x.device, dtype=torch.bfloat16)
+    _call("moe_amd_router_linear_backward_dw", d_logits.data_ptr(), x.data_ptr(), T, E, H,
+          ws.data_ptr(), ws.numel(), d_w.data_ptr(), _stream(x))
+    return d_w
+
+
 def router_softmax_topk(logits: torch.Tensor, top_k: int, renormalize: bool = True,
                         logit_offset: torch.Tensor | None = None,
                         tokens_per_expert: torch.Tensor | None = None):
@@ -325,12 +359,22 @@ def combine_backward(d_out, y, plan: RoutingPlan, topk_weights):
     return dy, dw
 
 
-def gather_backward(dxs, plan: RoutingPlan) -> torch.Tensor:
-    _need_cuda(dxs)
+def gather_backward(dxs, plan: RoutingPlan, addend: torch.Tensor | None = None) -> torch.Tensor:
+    """dx[t] = sum_k dxs[slot[t,k]] (fp32 sum, one rounding); with ``addend``
+    [T,H] (same dtype), dx[t] = round(round(sum) + addend[t])."""
+    _need_cuda(dxs, addend)
     T, K, E = plan.num_tokens, plan.top_k, plan.num_experts
     H = dxs.shape[1]
     dx = torch.empty(T, H, device=dxs.device, dtype=dxs.dtype)
-    _call("moe_amd_gather_backward", dxs.data_ptr(), plan.slot.data_ptr(),
-          plan.offsets.data_ptr(), T, K, E, H, _dtype_code(dxs.dtype), dx.data_ptr(),
-          _stream(dxs))
+    if addend is None:
+        _call("moe_amd_gather_backward", dxs.data_ptr(), plan.slot.data_ptr(),
+              plan.offsets.data_ptr(), T, K, E, H, _dtype_code(dxs.dtype), dx.data_ptr(),
+              _stream(dxs))
+    else:
+        if addend.dtype != dxs.dtype or tuple(addend.shape) != (T, H):
+            raise ValueError("gather_backward: addend must be [T,H] in d_xs' dtype")
+        addend = _contig(addend)
+        _call("moe_amd_gather_backward_add", dxs.data_ptr(), plan.slot.data_ptr(),
+              plan.offsets.data_ptr(), addend.data_ptr(), T, K, E, H, _dtype_code(dxs.dtype),
+              dx.data_ptr(), _stream(dxs))
     return dx

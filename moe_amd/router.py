@@ -36,8 +36,10 @@ class RouterLinearFunction(torch.autograd.Function):
     """logits = x . W^T on the MFMA kernel (bf16 inputs, fp32 accumulation),
     logits in bf16 (F.linear on bf16 tensors, src/models/modeling_qwen3_moe.py:
     268-270) or fp32 (F.linear(h.float(), W.float()), src/models/router.py:
-    107-109).  The backward is the matching torch linear backward: in bf16
-    for bf16 logits, in fp32 (then cast to the inputs' dtypes) for fp32."""
+    107-109).  The backward for bf16 logits runs on the MFMA dX and split-K dW
+    kernels (fp32 accumulation, one bf16 rounding, as F.linear's bf16
+    backward) where H is a multiple of 256 (dW: E <= 256), else torch in bf16;
+    for fp32 logits it is torch in fp32, cast to the inputs' dtypes."""
 
     @staticmethod
     def forward(ctx, x, weight, out_dtype):
@@ -57,10 +59,12 @@ class RouterLinearFunction(torch.autograd.Function):
                 dw = (g.t().contiguous() @ x.float()).to(weight.dtype)
         else:
             g = d_logits.to(x.dtype)
+            E, H = weight.shape
             if ctx.needs_input_grad[0]:
-                dx = g @ weight
+                dx = ops.router_linear_backward_dx(g, weight) if H % 256 == 0 else g @ weight
             if ctx.needs_input_grad[1]:
-                dw = g.t().contiguous() @ x
+                dw = (ops.router_linear_backward_dw(g, x) if H % 256 == 0 and E <= 256
+                      else g.t().contiguous() @ x)
         return dx, dw, None
 
 

@@ -194,3 +194,81 @@ def test_hip_gating_linear_matches_torch_gating():
     assert _rel(p_h, p_t) < 2e-2
     assert _rel(o_h[same], o_t[same]) < 2e-2
     assert _rel(g_h, g_t) < 5e-2
+    assert _rel(dx_h[same], dx_t[same]) < 5e-2
+
+
+def test_fused_softmax_layer_matches_composed_nodes():
+    """The one-node softmax layer (SoftmaxMoELayerFunction, chosen by moe_layer
+    for bf16 inputs) against the same arithmetic as three autograd nodes
+    (RouterLinearFunction -> SoftmaxTopKFunction -> MoEExpertsFunction): the
+    forward, the expert-weight and router-weight gradients are bit-identical;
+    d_x differs only through the gating linear's dX summation order (MFMA
+    kernel vs torch), i.e. within one bf16 rounding of the router term."""
+    from moe_amd.layer import SoftmaxMoELayerFunction
+    from moe_amd.router import RouterLinearFunction, SoftmaxTopKFunction
+    cfg = CONFIGS["l"].scaled(4096)
+    inp = make_inputs(cfg, seed=1, device=DEV)
+    outs = []
+    for fused in (True, False):
+        x = inp.x.clone().requires_grad_(True)
+        wr = inp.w_router.clone().requires_grad_(True)
+        w1 = inp.gate_up_proj.clone().requires_grad_(True)
+        w2 = inp.down_proj.clone().requires_grad_(True)
+        if fused:
+            out, probs, w, idx = SoftmaxMoELayerFunction.apply(x, wr, w1, w2, cfg.K, True, None)
+        else:
+            logits = RouterLinearFunction.apply(x, wr, torch.bfloat16)
+            probs, w, idx = SoftmaxTopKFunction.apply(logits, cfg.K, True, None)
+            out = experts_forward(x, idx, w, w1, w2)
+        out.backward(inp.dout)
+        outs.append((out.detach(), probs, idx, x.grad, wr.grad, w1.grad, w2.grad))
+    torch.cuda.synchronize()
+    a, b = outs
+    for i in (0, 1, 2, 4, 5, 6):
+        assert torch.equal(a[i], b[i]), i
+    assert _rel(a[3], b[3]) < 1e-2
+
+
+def test_router_linear_backward_dx_and_gather_add():
+    """The gating linear's dX kernel against fp32 torch (within one bf16
+    rounding), and the gather backward with an addend against
+    bf16(bf16(sum_k dxs[slot]) + addend), bit-exact."""
+    g = torch.Generator().manual_seed(7)
+    T, H, E, K = 4096, 2048, 128, 8
+    dl = torch.randn(T, E, generator=g).to(torch.bfloat16).to(DEV)
+    wr = (torch.randn(E, H, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    dx = ops.router_linear_backward_dx(dl, wr)
+    ref = dl.float() @ wr.float()
+    err = (dx.double() - ref.double()).abs()
+    assert bool((err <= ref.double().abs() * 2.0 ** -8 + 1e-5 * ref.abs().max().item()).all())
+    idx = torch.randint(0, E, (T, K), generator=g).to(DEV)
+    plan = ops.permute(idx, E)
+    dxs = torch.randn(T * K, H, generator=g).to(torch.bfloat16).to(DEV)
+    add = torch.randn(T, H, generator=g).to(torch.bfloat16).to(DEV)
+    got = ops.gather_backward(dxs, plan, addend=add)
+    plain = ops.gather_backward(dxs, plan)
+    want = (plain.float() + add.float()).to(torch.bfloat16)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("T,H,E", [(65536, 2048, 128), (1001, 512, 16), (37, 256, 8), (0, 256, 8),
+                                   (4096, 768, 256)])
+def test_router_linear_backward_dw(T, H, E):
+    """The gating linear's weight gradient (split over token chunks, fp32
+    partials) against fp32 torch on the same bf16 inputs: within one bf16
+    rounding of each element plus 1e-5 of the largest; run twice, bit-equal
+    (the chunk reduction order is fixed)."""
+    print(f"router dW T={T} H={H} E={E}", flush=True)
+    g = torch.Generator().manual_seed(T + H + E)
+    dl = torch.randn(T, E, generator=g).to(torch.bfloat16).to(DEV)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(DEV)
+    dw = ops.router_linear_backward_dw(dl, x)
+    dw2 = ops.router_linear_backward_dw(dl, x)
+    ref = dl.float().t().contiguous() @ x.float()
+    torch.cuda.synchronize()
+    assert dw.shape == (E, H) and dw.dtype == torch.bfloat16
+    assert torch.equal(dw, dw2)
+    err = (dw.double() - ref.double()).abs()
+    tol = ref.double().abs() * 2.0 ** -8 + 1e-5 * max(ref.abs().max().item(), 1.0)
+    assert bool((err <= tol).all()), float((err - tol).max())

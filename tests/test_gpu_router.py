@@ -194,3 +194,16 @@ def test_router_linear_rejects():
         ops.router_linear(x, torch.zeros(12, 128, dtype=torch.bfloat16, device=DEV))
     with pytest.raises(TypeError):
         ops.router_linear(x.float(), torch.zeros(8, 128, device=DEV))
+
+
+def test_router_linear_zero_tokens():
+    """No tokens: empty logits and an empty dX, no error."""
+    x = torch.empty(0, 256, dtype=torch.bfloat16, device=DEV)
+    wr = torch.randn(16, 256, device=DEV).to(torch.bfloat16)
+    assert ops.router_linear(x, wr, torch.float32).shape == (0, 16)
+    assert ops.router_linear(x, wr, torch.bfloat16).shape == (0, 16)
+    dl = torch.empty(0, 16, dtype=torch.bfloat16, device=DEV)
+    assert ops.router_linear_backward_dx(dl, wr).shape == (0, 256)
+    dw = ops.router_linear_backward_dw(dl, x)
+    torch.cuda.synchronize()
+    assert dw.shape == (16, 256) and not dw.any()
