@@ -492,15 +492,22 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
 
     // --------------------------------------------------------- main loop
     // Ring position h holds the column half (h = 2s) or the row half
-    // (h = 2s+1) of stage s, in slot h % 5.  Step kt waits until only the
-    // last-issued column half (stage kt+1) may still be in flight, so that
-    // both halves of stage kt (and, for G1DW, the row_src entries of stage
-    // kt+2) have landed; after the barrier the slots of stage kt-1 are free
-    // and receive the row half of stage kt+1 and the column half of stage
-    // kt+2.  Stages past the last one are still issued (their loads read
-    // zeros or in-bounds bytes that are never used) to keep the count exact.
+    // (h = 2s+1) of stage s, in slot h % 5.  Barrier B(s) comes after each
+    // wave has waited until only the last-issued column half (stage s+1)
+    // may still be in flight: stage s has landed everywhere, and every wave
+    // has finished reading stage s-1.  B(s+1) sits before the last k
+    // sub-step of stage s (whose fragments are already in registers), so
+    // that the first fragments of stage s+1 are read while those MFMAs run.
+    // Window W(s), the memory ops issued after B(s), is: the row_src
+    // entries of stage s+3 (G1DW), the DMA of the row half of stage s+1 and
+    // of the column half of stage s+2 (into stage s-1's slots), in this
+    // order, spread over 16 MFMA groups (the last sub-step of stage s-1 and
+    // the first three of stage s): issued in one burst they back up the
+    // texture pipe and stall MFMA issue.  Stages past the last one are
+    // still issued (their loads read zeros or in-bounds bytes that are
+    // never used) to keep the wait counts exact.
     if (cur.nk > 0) {
-      int tk_a[NTOK > 0 ? NTOK : 1], tk_b[NTOK > 0 ? NTOK : 1];
+      int tk_a[NTOK > 0 ? NTOK : 1], tk_b[NTOK > 0 ? NTOK : 1], tn[NTOK > 0 ? NTOK : 1];
       // The wait counts rely on issue order; sched_barrier keeps the
       // scheduler from interleaving the groups.
       fetch_tok(0, tk_a);
@@ -511,68 +518,93 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       issue_row(0);
       __builtin_amdgcn_sched_barrier(0);
       issue_col(1, tk_b);
-      for (int kt = 0; kt < cur.nk; ++kt) {
-        // lgkmcnt(0): this wave's reads of stage kt-1 are complete before
-        // the barrier lets other waves overwrite their slots.
-        WAIT_VMCNT_LGKM0(CPW);
-        __builtin_amdgcn_s_barrier();
-        const uint32_t sC = (uint32_t)((2 * kt) % NSLOT) * SLOT;      // column slot (bytes)
-        const uint32_t sR = (uint32_t)((2 * kt + 1) % NSLOT) * SLOT;  // row slot
-        char* rdst = slot_ptr(2 * kt + 3);  // row half of stage kt+1
-        char* cdst = slot_ptr(2 * kt + 4);  // column half of stage kt+2
-        int tn[NTOK > 0 ? NTOK : 1];
-        // The step's NOPS memory ops (row_src entries of stage kt+3, DMA of
-        // the row half of kt+1, DMA of the column half of kt+2, in this
-        // order) are spread over its 16 MFMA groups: issued in one burst
-        // they back up the texture pipe and stall the wave's MFMA issue.
-        const auto rs_row = stage_rsrc(rptr, rbytes, (uint32_t)(kt + 1) * rstep);
-        const auto rs_col = stage_rsrc(cptr, cbytes, (uint32_t)(kt + 2) * cstep);
-        auto mem_op = [&](int o) {
-          if (o < NTOK) {
-            if constexpr (MODE == G1DW) {
-              const int kr = (kt + 3) * BK + km_krow(wid + NW * o);
-              tn[o] = __builtin_amdgcn_raw_buffer_load_b32(isrc, (uint32_t)(kb_cur + kr) * 4, 0, 0);
-            }
-          } else if (o < NTOK + RPW) {
-            const int i = o - NTOK;
-            dma16(rs_row, roff[i], rdst + (wid + NW * i) * 1024);
-          } else {
-            const int i = o - NTOK - RPW;
-            dma16(rs_col, col_off(kt + 2, i, tk_a), cdst + (wid + NW * i) * 1024);
+      // Op o of window W(w); `tk` holds the row_src entries of stage w+2.
+      auto win_op = [&](int w, int o, const int (&tk)[NTOK > 0 ? NTOK : 1]) {
+        if (o < NTOK) {
+          if constexpr (MODE == G1DW) {
+            const int kr = (w + 3) * BK + km_krow(wid + NW * o);
+            tn[o] = __builtin_amdgcn_raw_buffer_load_b32(isrc, (uint32_t)(kb_cur + kr) * 4, 0, 0);
           }
-        };
-        // Fragments of sub-step ks+1 are read while the MFMAs of ks run,
-        // one column and one row fragment per MFMA group.
-        bf16x8 fa[2][TI], fb[2][TJ];
-        slot_bases(sC, sR);
+        } else if (o < NTOK + RPW) {
+          const int i = o - NTOK;
+          const auto rs = stage_rsrc(rptr, rbytes, (uint32_t)(w + 1) * rstep);
+          dma16(rs, roff[i], slot_ptr(2 * w + 3) + (wid + NW * i) * 1024);
+        } else {
+          const int i = o - NTOK - RPW;
+          const auto rs = stage_rsrc(cptr, cbytes, (uint32_t)(w + 2) * cstep);
+          dma16(rs, col_off(w + 2, i, tk), slot_ptr(2 * w + 4) + (wid + NW * i) * 1024);
+        }
+      };
+      // Issue order inside an MFMA group: two MFMAs, the group's memory
+      // ops, one MFMA, its fragment reads, the last MFMA (measured best
+      // among the orders tried).
+      auto group_order = [&]() {
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);  // VMEM read (the group's 0-2 ops)
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // DS read (2-4 fragment reads)
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      };
+      constexpr int GQ = BK / 16 - 1;  // groups before the last sub-step: NGRP - TI
+      bf16x8 fa[2][TI], fb[2][TJ];
+      WAIT_VMCNT_LGKM0(CPW);
+      __builtin_amdgcn_s_barrier();  // B(0)
+      slot_bases(0, (uint32_t)SLOT);
 #pragma unroll
-        for (int i = 0; i < TI; ++i) fa[0][i] = read_a(0, i);
+      for (int i = 0; i < TI; ++i) fa[0][i] = read_a(0, i);
 #pragma unroll
-        for (int j = 0; j < TJ; ++j) fb[0][j] = read_b(0, j);
+      for (int j = 0; j < TJ; ++j) fb[0][j] = read_b(0, j);
+      // the part of W(0) that belongs to the (absent) last sub-step of stage -1
 #pragma unroll
-        for (int ks = 0; ks < BK / 16; ++ks) {
+      for (int o = 0; o < TI * NOPS / NGRP; ++o) {
+        win_op(0, o, tk_a);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      for (int kt = 0; kt < cur.nk; ++kt) {
+        // Sub-steps 0..2 of stage kt; groups TI..NGRP-1 of W(kt).
+#pragma unroll
+        for (int ks = 0; ks < GQ; ++ks) {
 #pragma unroll
           for (int i = 0; i < TI; ++i) {
-            const int q = ks * TI + i;
+            const int q = TI + ks * TI + i;
 #pragma unroll
-            for (int o = q * NOPS / NGRP; o < (q + 1) * NOPS / NGRP; ++o) {
-              mem_op(o);
-              if (o + 1 < (q + 1) * NOPS / NGRP) __builtin_amdgcn_sched_barrier(0);
-            }
-            if (ks + 1 < BK / 16) {
-              fa[(ks + 1) & 1][i] = read_a(ks + 1, i);
-              if (i < TJ) fb[(ks + 1) & 1][i] = read_b(ks + 1, i);
-            }
+            for (int o = q * NOPS / NGRP; o < (q + 1) * NOPS / NGRP; ++o) win_op(kt, o, tk_a);
+            fa[(ks + 1) & 1][i] = read_a(ks + 1, i);
+            if (i < TJ) fb[(ks + 1) & 1][i] = read_b(ks + 1, i);
 #pragma unroll
             for (int j = 0; j < TJ; ++j)
               acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[ks & 1][i], fb[ks & 1][j],
                                                                   acc[i][j], 0, 0, 0);
+            group_order();
             __builtin_amdgcn_sched_barrier(0);
           }
         }
         if constexpr (NTOK > 0) {
 #pragma unroll
-          for (int i = 0; i < NTOK; ++i) tk_a[i] = tn[i];
+          for (int i = 0; i < NTOK; ++i) tk_a[i] = tn[i];  // row_src entries of stage kt+3
+        }
+        constexpr int LB = GQ & 1;  // fragment buffer of the last sub-step
+        static_assert(LB == 1, "sub-step 0 of the next stage reads into buffer 0");
+        // lgkmcnt(0): this wave's reads of stage kt are complete before the
+        // barrier lets other waves overwrite their slots.  (After the last
+        // stage this barrier, the reads of the stage past it and the ops of
+        // the window after it are junk, kept to make every iteration alike.)
+        WAIT_VMCNT_LGKM0(CPW);
+        __builtin_amdgcn_s_barrier();  // B(kt+1)
+        slot_bases((uint32_t)((2 * kt + 2) % NSLOT) * SLOT, (uint32_t)((2 * kt + 3) % NSLOT) * SLOT);
+        // Last sub-step of stage kt, groups 0..TI-1 of W(kt+1), and the
+        // fragments of sub-step 0 of stage kt+1.
+#pragma unroll
+        for (int i = 0; i < TI; ++i) {
+#pragma unroll
+          for (int o = i * NOPS / NGRP; o < (i + 1) * NOPS / NGRP; ++o) win_op(kt + 1, o, tk_a);
+          fa[0][i] = read_a(0, i);
+          if (i < TJ) fb[0][i] = read_b(0, i);
+#pragma unroll
+          for (int j = 0; j < TJ; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[1][i], fb[1][j], acc[i][j], 0, 0, 0);
+          group_order();
+          __builtin_amdgcn_sched_barrier(0);
         }
       }
     }
