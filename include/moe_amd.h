@@ -184,10 +184,13 @@ int moe_amd_gemm_down_backward_dx_dswiglu(const void* dy, const int32_t* offsets
                                           const void* gate_up, int64_t S, int E, int H, int I,
                                           int dtype, void* d_gate_up, void* stream);
 
-/* d_down_proj[e] = dy_e^T @ act_e  ([E,H,I]; zero for empty experts). */
+/* d_down_proj[e] = dy_e^T @ act_e  ([E,H,I]; zero for empty experts).
+ * With a tile plan (may be null) the tiles are claimed from its dW schedule:
+ * balanced under skewed routing; two dW launches that share one plan must
+ * not run concurrently. */
 int moe_amd_gemm_down_backward_dw(const void* dy, const void* act, const int32_t* offsets,
-                                  int64_t S, int E, int H, int I, int dtype, void* d_down_proj,
-                                  void* stream);
+                                  const void* tile_plan, int64_t S, int E, int H, int I,
+                                  int dtype, void* d_down_proj, void* stream);
 
 /* d_xs = d_gate_up @ gate_up_proj[e]  ([S,H]). */
 int moe_amd_gemm_gate_up_backward_dx(const void* d_gate_up, const int32_t* offsets,
@@ -196,11 +199,12 @@ int moe_amd_gemm_gate_up_backward_dx(const void* d_gate_up, const int32_t* offse
                                      void* stream);
 
 /* d_gate_up_proj[e] = d_gate_up_e^T @ xs_e, xs gathered from hidden_states
- * through row_src  ([E,2I,H]; zero for empty experts). */
+ * through row_src  ([E,2I,H]; zero for empty experts).  Tile plan as for
+ * moe_amd_gemm_down_backward_dw. */
 int moe_amd_gemm_gate_up_backward_dw(const void* d_gate_up, const void* hidden_states,
                                      const int32_t* row_src, int top_k, const int32_t* offsets,
-                                     int64_t T, int64_t S, int E, int H, int I, int dtype,
-                                     void* d_gate_up_proj, void* stream);
+                                     const void* tile_plan, int64_t T, int64_t S, int E, int H,
+                                     int I, int dtype, void* d_gate_up_proj, void* stream);
 
 /* ------------------------------------------------------------- combine */
 

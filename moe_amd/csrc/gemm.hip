@@ -93,6 +93,9 @@ struct GemmArgs {
   uint32_t tok_mul;      // n / topk == (n * tok_mul) >> tok_shift for 0 <= n < 2^31
   int tok_shift;         // 31 + ceil(log2(topk))
   int n_ct, n_rt, n_tiles;  // n_tiles: dW modes (host-known)
+  int* queue;            // G2DW/G1DW: this GEMM's 8 XCD tile counters + finished count (null: static walk)
+  const int* xstart;     // ... experts of XCD x: xorder[xstart[x] .. xstart[x+1])
+  const int* xorder;
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
@@ -192,12 +195,42 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
   const int H = p.H, I = p.I, I2 = 2 * p.I;
 
   // ------------------------------------------------------------ tile walk
+  // Static: the tile space is cut into 8 contiguous ranges, one per XCD
+  // (workgroups are dealt to the XCDs round-robin), walked with stride
+  // nslot.  Dynamic (dW GEMMs with a schedule): tile v belongs to expert
+  // xorder[v / tiles-per-expert]; each XCD's experts form a contiguous range
+  // of v that its workgroups claim one tile at a time from the XCD's
+  // counter, heaviest expert first, then from the other XCDs' counters once
+  // their own is exhausted.  Every workgroup stops when all 8 are.
   const int n_tiles = TOKEN ? (*p.tile_count) * p.n_ct : p.n_tiles;
   const int xcd = blockIdx.x & 7, nslot = gridDim.x >> 3;
+  const bool dyn = (MODE == G2DW || MODE == G1DW) && p.queue != nullptr;
+  const int per_e = p.n_rt * p.n_ct;
+  auto claim = [&]() -> int {
+    int* box = (int*)smem;  // free: the previous tile's epilogue ended with a barrier
+    if (tid == 0) {
+      int v = -1;
+      for (int k = 0; k < 8; ++k) {
+        const int x = (xcd + k) & 7;
+        const int e0 = p.xstart[x], n = (p.xstart[x + 1] - e0) * per_e;
+        if (n == 0) continue;
+        const int j = __hip_atomic_fetch_add(p.queue + x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (j < n) {
+          v = e0 * per_e + j;
+          break;
+        }
+      }
+      box[0] = v;
+    }
+    __syncthreads();
+    const int v = __builtin_amdgcn_readfirstlane(box[0]);
+    __syncthreads();  // read by every wave before the next tile's DMA may land here
+    return v;
+  };
   const int chunk = (n_tiles + 7) >> 3;
-  const int t_end = min(n_tiles, (xcd + 1) * chunk);
-  int t = xcd * chunk + (int)(blockIdx.x >> 3);
-  if (t >= t_end) return;
+  const int t_end = dyn ? 0 : min(n_tiles, (xcd + 1) * chunk);
+  int t = dyn ? claim() : xcd * chunk + (int)(blockIdx.x >> 3);
+  if (!dyn && t >= t_end) return;
 
   struct Tile {
     int e, row0, row_end, ct, kbeg, kend, nk;
@@ -218,9 +251,9 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       d.row_end = (int)min((int64_t)d.row0 + BR, p.T);
       d.kbeg = d.kend = 0;
     } else {
-      const int per_e = p.n_rt * p.n_ct;
-      d.e = tt / per_e;
-      const int rem = tt - d.e * per_e;
+      const int vi = tt / per_e;
+      d.e = dyn ? p.xorder[vi] : vi;
+      const int rem = tt - vi * per_e;
       const int rt = rem / p.n_ct;
       d.ct = rem - rt * p.n_ct;
       d.row0 = rt * BR;
@@ -480,7 +513,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
 
   f32x16 acc[TI][TJ];
 
-  for (; t < t_end; t += nslot) {
+  for (; dyn ? t >= 0 : t < t_end; t = dyn ? claim() : t + nslot) {
     const Tile cur = decode(t);
     setup(cur);
 #pragma unroll
@@ -788,6 +821,12 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       }
     }
     __syncthreads();  // staging reads done before the next tile's stages land
+  }
+  if (dyn && tid == 0) {
+    // The last workgroup to finish resets the counters for the next launch.
+    const int d = __hip_atomic_fetch_add(p.queue + 8, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (d == (int)gridDim.x - 1)
+      for (int k = 0; k < 9; ++k) __hip_atomic_store(p.queue + k, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -1117,9 +1156,20 @@ extern "C" int moe_amd_gemm_gate_up_backward_dx(const void* d_gate_up, const int
   return launch_token<G1DX>(a, S, E, BC, H, tile_plan, (hipStream_t)stream);
 }
 
+// The dW GEMMs claim tiles from the schedule in the tile plan when one is
+// given (balanced under skewed routing); without one they walk statically.
+void set_dw_schedule(GemmArgs& a, const void* tile_plan, int64_t S, int E, int which) {
+  if (!tile_plan) return;
+  int* sched = (int*)((char*)const_cast<void*>(tile_plan) + plan_sched_offset(S, E));
+  a.queue = sched + 16 * which;
+  a.xstart = sched + kSchedQueueInts;
+  a.xorder = sched + kSchedQueueInts + kSchedStartInts;
+}
+
 extern "C" int moe_amd_gemm_down_backward_dw(const void* dy, const void* act,
-                                             const int32_t* offsets, int64_t S, int E, int H,
-                                             int I, int dtype, void* d_down_proj, void* stream) {
+                                             const int32_t* offsets, const void* tile_plan,
+                                             int64_t S, int E, int H, int I, int dtype,
+                                             void* d_down_proj, void* stream) {
   const char* who = "gemm_down_backward_dw";
   int rc = check_common(S, E, H, I, dtype, who);
   if (rc) return rc;
@@ -1139,14 +1189,15 @@ extern "C" int moe_amd_gemm_down_backward_dw(const void* dy, const void* act,
   a.n_rt = (H + 255) / 256;
   a.n_ct = (I + BC - 1) / BC;
   a.n_tiles = E * a.n_rt * a.n_ct;
+  set_dw_schedule(a, tile_plan, S, E, 0);
   return launch<G2DW, 256>(a, a.n_tiles, (hipStream_t)stream);
 }
 
 extern "C" int moe_amd_gemm_gate_up_backward_dw(const void* d_gate_up, const void* hidden_states,
                                                 const int32_t* row_src, int top_k,
-                                                const int32_t* offsets, int64_t T, int64_t S,
-                                                int E, int H, int I, int dtype,
-                                                void* d_gate_up_proj, void* stream) {
+                                                const int32_t* offsets, const void* tile_plan,
+                                                int64_t T, int64_t S, int E, int H, int I,
+                                                int dtype, void* d_gate_up_proj, void* stream) {
   const char* who = "gemm_gate_up_backward_dw";
   int rc = check_common(S, E, H, I, dtype, who);
   if (rc) return rc;
@@ -1170,5 +1221,6 @@ extern "C" int moe_amd_gemm_gate_up_backward_dw(const void* d_gate_up, const voi
   a.n_rt = (2 * I + 255) / 256;
   a.n_ct = (H + BC - 1) / BC;
   a.n_tiles = E * a.n_rt * a.n_ct;
+  set_dw_schedule(a, tile_plan, S, E, 1);
   return launch<G1DW, 256>(a, a.n_tiles, (hipStream_t)stream);
 }

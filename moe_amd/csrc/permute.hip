@@ -141,6 +141,61 @@ __global__ __launch_bounds__(64) void tile_info_kernel(const int* __restrict__ o
     info[t] = make_int4(e, r0 + (t - t0) * bm, r1, 0);
 }
 
+// Single block: the dW-GEMM schedule.  Experts are sorted by an estimate of
+// their dW tile cost (rows + a fixed epilogue cost, in 64 log-spaced buckets,
+// heaviest first; order within a bucket is arbitrary: it changes which
+// workgroup computes a tile, never its result), then dealt to the 8 XCDs in
+// serpentine order (0..7, 7..0, ...), which balances the XCDs' sums.  Also
+// zeroes the GEMMs' queue counters.
+__global__ __launch_bounds__(1024) void dw_schedule_kernel(const int* __restrict__ counts, int E,
+                                                           int* __restrict__ queue,
+                                                           int* __restrict__ xstart,
+                                                           int* __restrict__ xorder) {
+  __shared__ int hist[64];
+  const int tid = threadIdx.x;
+  if (tid < kSchedQueueInts) queue[tid] = 0;
+  if (tid < 64) hist[tid] = 0;
+  // Experts per XCD under serpentine dealing depend on E only.
+  if (tid < kSchedStartInts) {
+    const int rounds = E / 8, rem = E % 8;
+    int acc = 0;
+    for (int x = 0; x < 8 && x < tid; ++x) {
+      const int lane = (rounds & 1) ? 7 - x : x;  // lane of XCD x in the last round
+      acc += rounds + (lane < rem ? 1 : 0);
+    }
+    xstart[tid] = tid <= 8 ? acc : E;
+  }
+  __syncthreads();
+  auto bucket = [](int n) {
+    const float c = (float)n + 192.f;  // rows, plus about three k-steps of epilogue
+    const int b = (int)(8.f * __log2f(c * (1.f / 192.f)));
+    return 63 - min(63, max(0, b));  // 0 = heaviest
+  };
+  for (int e = tid; e < E; e += blockDim.x) atomicAdd(&hist[bucket(counts[e])], 1);
+  __syncthreads();
+  if (tid == 0) {
+    int acc = 0;
+    for (int b = 0; b < 64; ++b) {
+      const int n = hist[b];
+      hist[b] = acc;
+      acc += n;
+    }
+  }
+  __syncthreads();
+  const int rounds = E / 8, rem = E % 8;
+  for (int e = tid; e < E; e += blockDim.x) {
+    const int pos = atomicAdd(&hist[bucket(counts[e])], 1);  // rank, heaviest first
+    const int r = pos / 8, l = pos % 8;
+    const int x = (r & 1) ? 7 - l : l;
+    int start = 0;
+    for (int y = 0; y < x; ++y) {
+      const int ly = (rounds & 1) ? 7 - y : y;
+      start += rounds + (ly < rem ? 1 : 0);
+    }
+    xorder[start + r] = e;
+  }
+}
+
 __global__ __launch_bounds__(64 * kWaves) void scatter_kernel(
     const int64_t* __restrict__ ids, int64_t S, int E, int64_t nch,
     const int* __restrict__ chunk_off, const int* __restrict__ offsets,
@@ -237,6 +292,9 @@ extern "C" int moe_amd_permute(const int64_t* topk_index, int64_t S, int E, void
                                               (int4*)(pb + plan_info_offset(S, E, 0)),
                                               (int4*)(pb + plan_info_offset(S, E, 1)),
                                               (int4*)(pb + plan_info_offset(S, E, 2)));
+  int* sched = (int*)(pb + plan_sched_offset(S, E));
+  dw_schedule_kernel<<<1, 1024, 0, st>>>(counts, E, sched, sched + kSchedQueueInts,
+                                         sched + kSchedQueueInts + kSchedStartInts);
   if (nch > 0) {
     const int blocks = (int)((nch + kWaves - 1) / kWaves);
     scatter_kernel<<<blocks, 64 * kWaves, lds, st>>>(topk_index, S, E, nch, chunk_hist,

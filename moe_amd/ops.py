@@ -298,14 +298,17 @@ def gemm_down_backward_dx_dswiglu(dy, plan: RoutingPlan, down_proj, gate_up):
     return dgu
 
 
-def gemm_down_backward_dw(dy, act, plan: RoutingPlan, down_proj_shape, out=None):
+def gemm_down_backward_dw(dy, act, plan: RoutingPlan, down_proj_shape, out=None,
+                          scheduled: bool = True):
+    """d_down_proj [E,H,I].  ``scheduled``: claim tiles from the plan's dW
+    schedule (balanced under skew); False walks the tiles statically."""
     _need_cuda(dy, act)
     E, H, I = down_proj_shape
     S = plan.num_rows
     dw = out if out is not None else torch.empty(E, H, I, device=dy.device, dtype=dy.dtype)
     _call("moe_amd_gemm_down_backward_dw", dy.data_ptr(), act.data_ptr(),
-          plan.offsets.data_ptr(), S, E, H, I, _dtype_code(dy.dtype), dw.data_ptr(),
-          _stream(dy))
+          plan.offsets.data_ptr(), plan.tile_plan.data_ptr() if scheduled else None, S, E, H, I,
+          _dtype_code(dy.dtype), dw.data_ptr(), _stream(dy))
     return dw
 
 
@@ -320,13 +323,16 @@ def gemm_gate_up_backward_dx(dgu, plan: RoutingPlan, gate_up_proj):
     return dxs
 
 
-def gemm_gate_up_backward_dw(dgu, x, plan: RoutingPlan, gate_up_proj_shape, out=None):
+def gemm_gate_up_backward_dw(dgu, x, plan: RoutingPlan, gate_up_proj_shape, out=None,
+                             scheduled: bool = True):
+    """d_gate_up_proj [E,2I,H]; ``scheduled`` as for gemm_down_backward_dw."""
     _need_cuda(dgu, x)
     E, I2, H = gate_up_proj_shape
     S = plan.num_rows
     dw = out if out is not None else torch.empty(E, I2, H, device=dgu.device, dtype=dgu.dtype)
     _call("moe_amd_gemm_gate_up_backward_dw", dgu.data_ptr(), x.data_ptr(),
-          plan.row_src.data_ptr(), plan.top_k, plan.offsets.data_ptr(), plan.num_tokens, S,
+          plan.row_src.data_ptr(), plan.top_k, plan.offsets.data_ptr(),
+          plan.tile_plan.data_ptr() if scheduled else None, plan.num_tokens, S,
           E, H, I2 // 2, _dtype_code(dgu.dtype), dw.data_ptr(), _stream(dgu))
     return dw
 
