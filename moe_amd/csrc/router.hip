@@ -73,25 +73,39 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void softmax_topk_kernel(
     int64_t T, int E, int K, int renorm, float* __restrict__ probs, float* __restrict__ topk_w,
     int64_t* __restrict__ topk_idx, float* __restrict__ tpe) {
   extern __shared__ int hist[];  // [E] when tpe != nullptr
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // token index stays scalar
   if (tpe) {
     for (int e = threadIdx.x; e < E; e += blockDim.x) hist[e] = 0;
     __syncthreads();
   }
   const int64_t nwaves = (int64_t)gridDim.x * kWavesPerBlock;
-  for (int64_t t = (int64_t)blockIdx.x * kWavesPerBlock + wid; t < T; t += nwaves) {
+  // Each wave walks its tokens with the next token's logits already in
+  // flight while the current one is ranked.
+  float raw[NV];
+  auto fetch = [&](int64_t tt) {
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int e = j * 64 + lane;
+      raw[j] = e < E ? load_logit(logits, logits_dtype, tt * E + e) : 0.f;
+    }
+  };
+  int64_t t = (int64_t)blockIdx.x * kWavesPerBlock + wid;
+  if (t < T) fetch(t);
+  for (; t < T; t += nwaves) {
     float v[NV];
     uint64_t taken = 0;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
       int e = j * 64 + lane;
       if (e < E) {
-        v[j] = load_logit(logits, logits_dtype, t * E + e) + (offset ? offset[e] : 0.0f);
+        v[j] = raw[j] + (offset ? offset[e] : 0.0f);
       } else {
         v[j] = -INFINITY;
         taken |= 1ull << j;
       }
     }
+    if (t + nwaves < T) fetch(t + nwaves);
     float m = -INFINITY;
 #pragma unroll
     for (int j = 0; j < NV; ++j) m = fmaxf(m, v[j]);
@@ -140,27 +154,39 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void softmax_topk_kernel(
   }
 }
 
-template <int NV>
+template <int NV, bool GROUPS>
 __global__ __launch_bounds__(64 * kWavesPerBlock) void sigmoid_topk_kernel(
     const float* __restrict__ logits, const float* __restrict__ bias, int64_t T, int E, int K,
     int renorm, float scaling, int num_groups, int group_topk, float* __restrict__ scores,
     void* __restrict__ topk_w, int w_dtype, int64_t* __restrict__ topk_idx,
     float* __restrict__ tpe) {
   extern __shared__ int hist[];
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // token index stays scalar
   if (tpe) {
     for (int e = threadIdx.x; e < E; e += blockDim.x) hist[e] = 0;
     __syncthreads();
   }
   const int64_t nwaves = (int64_t)gridDim.x * kWavesPerBlock;
-  for (int64_t t = (int64_t)blockIdx.x * kWavesPerBlock + wid; t < T; t += nwaves) {
+  // Next token's logits in flight while the current one is ranked.
+  float raw[NV];
+  auto fetch = [&](int64_t tt) {
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int e = j * 64 + lane;
+      raw[j] = e < E ? logits[tt * E + e] : 0.f;
+    }
+  };
+  int64_t t = (int64_t)blockIdx.x * kWavesPerBlock + wid;
+  if (t < T) fetch(t);
+  for (; t < T; t += nwaves) {
     float s[NV], b[NV];
     uint64_t taken = 0;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
       int e = j * 64 + lane;
       if (e < E) {
-        s[j] = sigmoidf_(logits[t * E + e]);
+        s[j] = sigmoidf_(raw[j]);
         scores[t * E + e] = s[j];
         b[j] = s[j] + (bias ? bias[e] : 0.0f);
       } else {
@@ -169,7 +195,8 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void sigmoid_topk_kernel(
         taken |= 1ull << j;
       }
     }
-    if (num_groups > 0) {
+    if (t + nwaves < T) fetch(t + nwaves);
+    if (GROUPS) {
       // Group-limited selection (router.py:22-70): score each group by the
       // sum of its top (K / group_topk) biased scores, keep group_topk groups.
       const int eg = E / num_groups, per = K / group_topk;
@@ -343,6 +370,15 @@ int grid_for(int64_t T) {
   return (int)blocks;
 }
 
+// Forward routers: about 8 tokens per wave, so that the per-block histogram
+// set-up and flush are amortised and each wave has a next token to prefetch.
+int grid_fwd(int64_t T) {
+  int64_t blocks = (T + kWavesPerBlock * 8 - 1) / (kWavesPerBlock * 8);
+  if (blocks > 4096) blocks = 4096;
+  if (blocks < 1) blocks = 1;
+  return (int)blocks;
+}
+
 #define MOE_DISPATCH_NV(E, KERNEL, ...)                          \
   do {                                                           \
     int nv_ = ((E) + 63) / 64;                                   \
@@ -353,6 +389,18 @@ int grid_for(int64_t T) {
     else if (nv_ <= 16) KERNEL<16><<<__VA_ARGS__;                \
     else if (nv_ <= 32) KERNEL<32><<<__VA_ARGS__;                \
     else KERNEL<64><<<__VA_ARGS__;                               \
+  } while (0)
+
+#define MOE_DISPATCH_NV_G(E, G, KERNEL, ...)                     \
+  do {                                                           \
+    int nv_ = ((E) + 63) / 64;                                   \
+    if (nv_ <= 1) KERNEL<1, G><<<__VA_ARGS__;                    \
+    else if (nv_ <= 2) KERNEL<2, G><<<__VA_ARGS__;               \
+    else if (nv_ <= 4) KERNEL<4, G><<<__VA_ARGS__;               \
+    else if (nv_ <= 8) KERNEL<8, G><<<__VA_ARGS__;               \
+    else if (nv_ <= 16) KERNEL<16, G><<<__VA_ARGS__;             \
+    else if (nv_ <= 32) KERNEL<32, G><<<__VA_ARGS__;             \
+    else KERNEL<64, G><<<__VA_ARGS__;                            \
   } while (0)
 
 int check_router_shape(int64_t T, int E, int K) {
@@ -382,7 +430,7 @@ extern "C" int moe_amd_router_softmax_topk(const void* logits, int logits_dtype,
               "router_softmax_topk: null pointer");
   if (T == 0) return MOE_OK;
   size_t shm = tokens_per_expert ? (size_t)E * sizeof(int) : 0;
-  MOE_DISPATCH_NV(E, softmax_topk_kernel, grid_for(T), 64 * kWavesPerBlock, shm,
+  MOE_DISPATCH_NV(E, softmax_topk_kernel, grid_fwd(T), 64 * kWavesPerBlock, shm,
                   (hipStream_t)stream >>>(logits, logits_dtype, logit_offset, T, E, K,
                                           renormalize, probs, topk_weights, topk_index,
                                           tokens_per_expert));
@@ -430,11 +478,19 @@ extern "C" int moe_amd_router_sigmoid_topk(const float* logits, const float* exp
   if (T == 0) return MOE_OK;
   if (!(scaling_factor > 0.f)) scaling_factor = 0.f;
   size_t shm = tokens_per_expert ? (size_t)E * sizeof(int) : 0;
-  MOE_DISPATCH_NV(E, sigmoid_topk_kernel, grid_for(T), 64 * kWavesPerBlock, shm,
-                  (hipStream_t)stream >>>(logits, expert_bias, T, E, K, renormalize,
-                                          scaling_factor, num_groups, group_topk, scores,
-                                          topk_weights, weights_dtype, topk_index,
-                                          tokens_per_expert));
+  if (num_groups > 0) {
+    MOE_DISPATCH_NV_G(E, true, sigmoid_topk_kernel, grid_fwd(T), 64 * kWavesPerBlock, shm,
+                      (hipStream_t)stream >>>(logits, expert_bias, T, E, K, renormalize,
+                                              scaling_factor, num_groups, group_topk, scores,
+                                              topk_weights, weights_dtype, topk_index,
+                                              tokens_per_expert));
+  } else {
+    MOE_DISPATCH_NV_G(E, false, sigmoid_topk_kernel, grid_fwd(T), 64 * kWavesPerBlock, shm,
+                      (hipStream_t)stream >>>(logits, expert_bias, T, E, K, renormalize,
+                                              scaling_factor, num_groups, group_topk, scores,
+                                              topk_weights, weights_dtype, topk_index,
+                                              tokens_per_expert));
+  }
   return check_launch("router_sigmoid_topk");
 }
 
