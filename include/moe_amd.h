@@ -238,6 +238,56 @@ int moe_amd_gather_backward_add(const void* d_xs, const int32_t* slot, const int
                                 const void* addend, int64_t T, int K, int E, int H, int dtype,
                                 void* d_x, void* stream);
 
+/* ---------------------------------------------------- routing consumers */
+
+/* One pass over a layer's router probabilities probs [T,E] (fp32 or bf16):
+ * counts[e] = sum over tokens of w[t] * (e among the token's top K) and
+ * prob_sums[e] = sum_t w[t] * probs[t,e] (w = token_weights, or 1 when
+ * null), margin[0] = sum_t (v_K - v_(K+1)) and margin[1] = min_t of it (the
+ * K-th and (K+1)-th largest probabilities; 0 and +inf when K == E).  Output
+ * in fp64, reduced in a fixed order (deterministic).  Replaces the
+ * topk/one_hot/mean chains of src/models/load_balancing.py:45-88 and
+ * src/utils/routing_stats.py:53-80, :143-191. */
+size_t moe_amd_topk_stats_workspace_size(int64_t T, int E);
+int moe_amd_topk_stats(const void* probs, int probs_dtype, const float* token_weights, int64_t T,
+                       int E, int K, void* workspace, size_t workspace_bytes, double* counts,
+                       double* prob_sums, double* margin, void* stream);
+
+/* DeepSeek-V3 sequence-wise loss statistics of one layer (scores [T,E], T =
+ * B sequences of S tokens): s' = s / (sum_e s + 1e-20) per token; counts[b,e]
+ * = selections of e in sequence b (selected [T,K] int64 routed indices, or
+ * the top K of s' when null) and mean_scores[b,e] = mean over the sequence
+ * of s'[t,e] (fp64).  src/models/load_balancing.py:134-166. */
+size_t moe_amd_seq_stats_workspace_size(int64_t T, int E, int B);
+int moe_amd_seq_stats(const void* scores, int scores_dtype, const int64_t* selected, int64_t T,
+                      int E, int K, int B, void* workspace, size_t workspace_bytes,
+                      double* counts, double* mean_scores, void* stream);
+
+/* Backward of the sequence-wise loss through the normalisation: with g[t,e]
+ * = coef[b(t),e] the loss gradient w.r.t. s'[t,e], d_scores[t,e] =
+ * (g[t,e] - sum_f g[t,f] s'[t,f]) / (sum_f s[t,f] + 1e-20), in scores'
+ * dtype.  Autograd of load_balancing.py:143. */
+int moe_amd_seq_aux_backward(const void* scores, int scores_dtype, const double* coef, int64_t T,
+                             int E, int B, void* d_scores, void* stream);
+
+/* Backward of the Switch loss: grad[t,e] = coef[e] * w[t] (w = 1 when
+ * token_weights is null), in grad_dtype.  Autograd of load_balancing.py:87-88. */
+int moe_amd_switch_aux_backward(const double* coef, const float* token_weights, int64_t T, int E,
+                                int grad_dtype, void* grad, void* stream);
+
+/* Aux-loss-free balancing step for L routers at once (train.py:79-139 without
+ * the DDP all-reduce): counts[l] and biases[l] are device pointers to each
+ * router's fp32 [E] local_tokens_per_expert and expert_bias (the two arrays
+ * of L pointers live in device memory).  Per layer (is_global 0) bias +=
+ * sign(mean(counts[l]) - counts[l]) * rate; pooled (is_global 1, alpha 0)
+ * with the counts summed over layers; blended (alpha > 0) alpha * per-layer
+ * + (1 - alpha) * pooled, in fp32 in the reference's operation order.
+ * Counts are zeroed; stats = mean, unbiased std, min, max of all new biases
+ * (fp64). */
+int moe_amd_update_expert_biases(float* const* counts, float* const* biases, int L, int E,
+                                 float update_rate, int is_global, double alpha, double* stats,
+                                 void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -63,6 +63,13 @@ SIGNATURES: dict[str, tuple] = {
         _i, [_p, _p, _p, _p, _p, _i, _i64, _i, _i, _i, _i, _p, _p, _p]),
     "moe_amd_gather_backward": (_i, [_p, _p, _p, _i64, _i, _i, _i, _i, _p, _p]),
     "moe_amd_gather_backward_add": (_i, [_p, _p, _p, _p, _i64, _i, _i, _i, _i, _p, _p]),
+    "moe_amd_topk_stats_workspace_size": (_sz, [_i64, _i]),
+    "moe_amd_topk_stats": (_i, [_p, _i, _p, _i64, _i, _i, _p, _sz, _p, _p, _p, _p]),
+    "moe_amd_seq_stats_workspace_size": (_sz, [_i64, _i, _i]),
+    "moe_amd_seq_stats": (_i, [_p, _i, _p, _i64, _i, _i, _i, _p, _sz, _p, _p, _p]),
+    "moe_amd_seq_aux_backward": (_i, [_p, _i, _p, _i64, _i, _i, _p, _p]),
+    "moe_amd_switch_aux_backward": (_i, [_p, _p, _i64, _i, _i, _p, _p]),
+    "moe_amd_update_expert_biases": (_i, [_p, _p, _i, _i, _f, _i, ctypes.c_double, _p, _p]),
 }
 
 _lock = threading.Lock()
