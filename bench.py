@@ -12,8 +12,11 @@ bf16.
 Prints ONE JSON line on stdout (progress goes to stderr).  The line carries
 the layer throughput (tokens/s), per-kernel HIP-event timings over the timed
 steps, the roofline of the dominant grouped GEMM against the 2.5 PFLOP/s
-dense bf16 MFMA peak, and a CPU baseline: the oracle restatement of the
-reference algorithm timed on the host cores on a bounded token sample.
+dense bf16 MFMA peak, a CPU baseline (the oracle restatement of the
+reference algorithm timed on the host cores on a bounded token sample), and,
+outside the timed steps, the times of the routing consumers (load-balancing
+losses, routing statistics, expert-bias update) on the layer's router
+output.
 """
 from __future__ import annotations
 
@@ -117,6 +120,64 @@ RECORDED_TRAFFIC_L = {
 def recorded_traffic(cfg_name: str, kernel: str):
     """Measured HBM bytes per launch of `kernel` (L shape only), else None."""
     return RECORDED_TRAFFIC_L.get(kernel) if cfg_name.startswith("L") else None
+
+
+def probs_for_consumers(cfg, x, wr, inp):
+    """The layer's router probabilities (or sigmoid scores) at the bench shape."""
+    from moe_amd import ops
+    with torch.no_grad():
+        if cfg.router == "softmax":
+            logits = ops.router_linear(x.detach(), wr.detach(), torch.bfloat16)
+            probs, _, _ = ops.router_softmax_topk(logits, cfg.K, True, inp.logit_offset)
+            return probs
+        logits = torch.nn.functional.linear(x.detach().float(), wr.detach().float())
+        return torch.sigmoid(logits)
+
+
+def routing_consumers(cfg, probs, dev, reps: int = 5) -> dict:
+    """HIP-event times of the routing consumers on one layer at the bench
+    shape: Switch and sequence-wise load-balancing losses (fwd+bwd), routing
+    statistics, and the bias update of 48 routers (the depth of
+    Qwen3-30B-A3B); achieved GB/s of the [T, E] statistics pass."""
+    from moe_amd import balancing as Bal
+    from moe_amd import ops
+    T, E, K = probs.shape[0], probs.shape[1], cfg.K
+    seqs = max(1, T // 8192)
+    p = probs.detach().requires_grad_(True)
+    routers = torch.nn.Module()
+    routers.layers = torch.nn.ModuleList()
+    for _ in range(48):
+        m = torch.nn.Module()
+        m.register_buffer("expert_bias", torch.zeros(E, device=dev))
+        m.register_buffer("local_tokens_per_expert",
+                          torch.full((E,), float(T * K // E), device=dev))
+        routers.layers.append(m)
+
+    def once():
+        Bal.load_balancing_loss_func((p,), E, K).backward()
+        Bal.seq_load_balancing_loss_func((p,), E, K, batch_size=seqs).backward()
+        Bal.compute_routing_stats((p.detach(),), K)
+        Bal.update_expert_biases(routers, 1e-3)
+
+    once()
+    torch.cuda.synchronize()
+    events: list = []
+    ops.record_kernel_times(events)
+    for _ in range(reps):
+        once()
+    torch.cuda.synchronize()
+    ops.record_kernel_times(None)
+    per: dict[str, list[float]] = {}
+    for name, s, e in events:
+        per.setdefault(name.replace("moe_amd_", ""), []).append(s.elapsed_time(e))
+    out = {"shape": {"T": T, "E": E, "K": K, "sequences": seqs, "routers": 48},
+           "kernels_ms": {k: round(sum(v) / len(v), 4) for k, v in per.items()}}
+    st = out["kernels_ms"].get("topk_stats")
+    if st:
+        nbytes = T * E * probs.element_size()
+        out["topk_stats_gbs"] = round(nbytes / st / 1e6, 1)
+        out["topk_stats_frac_hbm"] = round(nbytes / st / 1e6 / PEAK_HBM_GBS, 4)
+    return out
 
 
 def main():
@@ -234,6 +295,7 @@ def main():
                      "traffic": recorded_traffic(cfg.name, dom.replace("moe_amd_", ""))},
         "kernels": kernels,
     }
+    result["routing_consumers"] = routing_consumers(cfg, probs_for_consumers(cfg, x, wr, inp), dev)
     if not args.no_cpu_baseline:
         log(f"[bench] CPU baseline on {args.cpu_tokens} tokens ...")
         result["cpu_baseline"] = cpu_baseline(cfg, args.cpu_tokens)

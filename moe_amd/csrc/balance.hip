@@ -26,7 +26,7 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kTokensPerWave = 8;  // topk_stats: tokens per wave (grid sizing)
-constexpr int kSeqChunk = 256;     // seq_stats: tokens per block
+constexpr int kSeqChunk = 64;      // seq_stats: tokens per block
 
 __device__ __forceinline__ float load_val(const void* p, int dtype, int64_t i) {
   return dtype == MOE_DTYPE_BF16 ? bf2f(((const bf16*)p)[i]) : ((const float*)p)[i];
@@ -131,29 +131,46 @@ __global__ __launch_bounds__(64 * kWaves) void topk_stats_kernel(
   }
 }
 
-// Sums the block partials in block order: counts, sums [E] and the margin.
-__global__ __launch_bounds__(256) void topk_stats_finalize_kernel(
+// Fixed-order wave reduction of one fp64 value per lane (butterfly).
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// One wave per expert (blocks 0..E-1): lane l sums the partials of blocks l,
+// l+64, ... in order, then the lanes are combined by a fixed butterfly.
+// Block E reduces the margin partials the same way.
+__global__ __launch_bounds__(64) void topk_stats_finalize_kernel(
     const float* __restrict__ part_cnt, const float* __restrict__ part_sum,
     const double* __restrict__ part_margin, int nblk, int E, double* __restrict__ counts,
     double* __restrict__ sums, double* __restrict__ margin) {
-  const int e = blockIdx.x * blockDim.x + threadIdx.x;
+  const int lane = threadIdx.x, e = blockIdx.x;
   if (e < E) {
     double c = 0.0, s = 0.0;
-    for (int b = 0; b < nblk; ++b) {
+    for (int b = lane; b < nblk; b += 64) {
       c += (double)part_cnt[(size_t)b * E + e];
       s += (double)part_sum[(size_t)b * E + e];
     }
-    counts[e] = c;
-    sums[e] = s;
-  }
-  if (e == 0) {
+    c = wave_sum_f64(c);
+    s = wave_sum_f64(s);
+    if (lane == 0) {
+      counts[e] = c;
+      sums[e] = s;
+    }
+  } else {
     double s = 0.0, m = INFINITY;
-    for (int b = 0; b < nblk; ++b) {
+    for (int b = lane; b < nblk; b += 64) {
       s += part_margin[b * 2];
       m = fmin(m, part_margin[b * 2 + 1]);
     }
-    margin[0] = s;
-    margin[1] = m;
+    s = wave_sum_f64(s);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmin(m, __shfl_xor(m, o, 64));
+    if (lane == 0) {
+      margin[0] = s;
+      margin[1] = m;
+    }
   }
 }
 
@@ -223,21 +240,26 @@ __global__ __launch_bounds__(64 * kWaves) void seq_stats_kernel(
   block_combine<NV>(psum, E, buf, part_sum + slot);
 }
 
-// counts[b][e] = sum over chunks, mean[b][e] = sum over chunks / S.
-__global__ __launch_bounds__(256) void seq_stats_finalize_kernel(
+// One wave per (b, e): counts[b][e] = sum over chunks, mean[b][e] = sum over
+// chunks / S, in the fixed order of wave_sum_f64.
+__global__ __launch_bounds__(64) void seq_stats_finalize_kernel(
     const float* __restrict__ part_cnt, const float* __restrict__ part_sum, int nchunk, int B,
     int E, int64_t S, double* __restrict__ counts, double* __restrict__ mean) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (int64_t)B * E) return;
+  const int lane = threadIdx.x;
+  const int64_t i = blockIdx.x;
   const int b = (int)(i / E), e = (int)(i % E);
   double c = 0.0, s = 0.0;
-  for (int k = 0; k < nchunk; ++k) {
+  for (int k = lane; k < nchunk; k += 64) {
     const size_t o = ((size_t)b * nchunk + k) * E + e;
     c += (double)part_cnt[o];
     s += (double)part_sum[o];
   }
-  counts[i] = c;
-  mean[i] = s / (double)S;
+  c = wave_sum_f64(c);
+  s = wave_sum_f64(s);
+  if (lane == 0) {
+    counts[i] = c;
+    mean[i] = s / (double)S;
+  }
 }
 
 // d s from d s' through s' = s / (sum s + eps): (g - <g, s'>) / (sum s + eps),
@@ -440,14 +462,12 @@ extern "C" int moe_amd_topk_stats(const void* probs, int probs_dtype, const floa
   float* ps = pc + (size_t)nb * E;
   double* pm = (double*)((char*)workspace + align_up((size_t)nb * E * 2 * sizeof(float), 16));
   if (T == 0) {
-    topk_stats_finalize_kernel<<<(E + 255) / 256, 256, 0, st>>>(pc, ps, pm, 0, E, counts,
-                                                                prob_sums, margin);
+    topk_stats_finalize_kernel<<<E + 1, 64, 0, st>>>(pc, ps, pm, 0, E, counts, prob_sums, margin);
     return check_launch(who);
   }
   MOE_DISPATCH_NV_B(E, topk_stats_kernel, nb, 64 * kWaves, 0, st>>>(
       probs, probs_dtype, token_weights, T, E, K, pc, ps, pm));
-  topk_stats_finalize_kernel<<<(E + 255) / 256, 256, 0, st>>>(pc, ps, pm, nb, E, counts,
-                                                              prob_sums, margin);
+  topk_stats_finalize_kernel<<<E + 1, 64, 0, st>>>(pc, ps, pm, nb, E, counts, prob_sums, margin);
   return check_launch(who);
 }
 
@@ -472,15 +492,15 @@ extern "C" int moe_amd_seq_stats(const void* scores, int scores_dtype,
               "%s: workspace of %zu bytes needed", who, need);
   const int64_t S = T / B;
   const int nc = (int)seq_chunks(S);
-  MOE_REQUIRE(nc < 65536 && B < 65536, MOE_ERR_UNSUPPORTED, "%s: grid too large", who);
+  MOE_REQUIRE(nc < 65536 && B < 65536 && (int64_t)B * E < ((int64_t)1 << 31), MOE_ERR_UNSUPPORTED,
+              "%s: grid too large", who);
   hipStream_t st = (hipStream_t)stream;
   float* pc = (float*)workspace;
   float* ps = pc + (size_t)B * nc * E;
   MOE_DISPATCH_NV_B(E, seq_stats_kernel, dim3(nc, B), 64 * kWaves, 0, st>>>(
       scores, scores_dtype, selected, S, E, K, pc, ps));
-  const int64_t n = (int64_t)B * E;
-  seq_stats_finalize_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(pc, ps, nc, B, E, S,
-                                                                         counts, mean_scores);
+  seq_stats_finalize_kernel<<<(unsigned)((int64_t)B * E), 64, 0, st>>>(pc, ps, nc, B, E, S,
+                                                                        counts, mean_scores);
   return check_launch(who);
 }
 
