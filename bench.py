@@ -58,6 +58,7 @@ def hbm_bytes(name: str, cfg) -> float:
         "moe_amd_combine": S * H * b + S * 8 + T * H * b,
         "moe_amd_combine_backward": T * H * b + 2 * S * H * b + S * 12,
         "moe_amd_gather_backward": S * H * b + S * 4 + T * H * b,
+        "moe_amd_gather_backward_add": S * H * b + S * 4 + 2 * T * H * b,
         "moe_amd_permute": S * 8 + S * 4 * 2 + E * 4,
     }
     return per.get(name, 0.0)

@@ -45,7 +45,25 @@ __device__ __forceinline__ float load_w(const void* w, int wdt, int64_t i) {
   return wdt == MOE_DTYPE_BF16 ? bf2f(((const bf16*)w)[i]) : ((const float*)w)[i];
 }
 
-template <typename T>
+// The K routed rows of token t (slot and weight), read once by lanes 0..K-1
+// and made wave-uniform, so that all K row loads of a step can be issued
+// before any of them is consumed.
+template <int KM>
+__device__ __forceinline__ void token_rows(const int* __restrict__ slot, const void* __restrict__ w,
+                                           int wdt, int64_t t, int lane, int (&s)[KM],
+                                           float (&wk)[KM]) {
+  const int my_s = lane < KM ? slot[t * KM + lane] : 0;
+  const float my_w = (w && lane < KM) ? load_w(w, wdt, t * KM + lane) : 0.f;
+#pragma unroll
+  for (int k = 0; k < KM; ++k) {
+    s[k] = __builtin_amdgcn_readlane(my_s, k);
+    wk[k] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_w), k));
+  }
+}
+
+// KM > 0: the top-k is KM (all loads of a row chunk in flight at once);
+// KM == 0: any K, rows loaded one after the other.
+template <typename T, int KM>
 __global__ __launch_bounds__(64 * kWaves) void combine_kernel(
     const T* __restrict__ y, const int* __restrict__ slot, const int* __restrict__ offsets,
     const void* __restrict__ w, int wdt, int64_t ntok, int K, int E, int H, T* __restrict__ out) {
@@ -54,29 +72,55 @@ __global__ __launch_bounds__(64 * kWaves) void combine_kernel(
   const int nvalid = offsets[E];
   const int64_t nw = (int64_t)gridDim.x * kWaves;
   for (int64_t t = (int64_t)blockIdx.x * kWaves + wid; t < ntok; t += nw) {
-    for (int h0 = lane * N; h0 < H; h0 += 64 * N) {
-      float acc[N];
+    if constexpr (KM > 0) {
+      int sk[KM];
+      float wk[KM];
+      token_rows<KM>(slot, w, wdt, t, lane, sk, wk);
+      for (int h0 = lane * N; h0 < H; h0 += 64 * N) {
+        float v[KM][N];
 #pragma unroll
-      for (int i = 0; i < N; ++i) acc[i] = 0.f;
-      for (int k = 0; k < K; ++k) {
-        const int s = slot[t * K + k];
-        if (s >= nvalid) continue;  // sentinel: masked to zero in the reference
-        const float wk = load_w(w, wdt, t * K + k);
-        float v[N];
-        Vec<T>::load(y + (int64_t)s * H + h0, v);
+        for (int k = 0; k < KM; ++k)
+          if (sk[k] < nvalid) Vec<T>::load(y + (int64_t)sk[k] * H + h0, v[k]);
+        float acc[N];
 #pragma unroll
-        for (int i = 0; i < N; ++i) {
-          float prod = v[i] * wk;
-          if (wdt == MOE_DTYPE_BF16 && sizeof(T) == 2) prod = round_bf(prod);
-          acc[i] += prod;
+        for (int i = 0; i < N; ++i) acc[i] = 0.f;
+#pragma unroll
+        for (int k = 0; k < KM; ++k) {
+          if (sk[k] >= nvalid) continue;  // sentinel: masked to zero in the reference
+#pragma unroll
+          for (int i = 0; i < N; ++i) {
+            float prod = v[k][i] * wk[k];
+            if (wdt == MOE_DTYPE_BF16 && sizeof(T) == 2) prod = round_bf(prod);
+            acc[i] += prod;
+          }
         }
+        Vec<T>::store(out + t * H + h0, acc);
       }
-      Vec<T>::store(out + t * H + h0, acc);
+    } else {
+      for (int h0 = lane * N; h0 < H; h0 += 64 * N) {
+        float acc[N];
+#pragma unroll
+        for (int i = 0; i < N; ++i) acc[i] = 0.f;
+        for (int k = 0; k < K; ++k) {
+          const int s = slot[t * K + k];
+          if (s >= nvalid) continue;  // sentinel: masked to zero in the reference
+          const float wk = load_w(w, wdt, t * K + k);
+          float v[N];
+          Vec<T>::load(y + (int64_t)s * H + h0, v);
+#pragma unroll
+          for (int i = 0; i < N; ++i) {
+            float prod = v[i] * wk;
+            if (wdt == MOE_DTYPE_BF16 && sizeof(T) == 2) prod = round_bf(prod);
+            acc[i] += prod;
+          }
+        }
+        Vec<T>::store(out + t * H + h0, acc);
+      }
     }
   }
 }
 
-template <typename T>
+template <typename T, int KM>
 __global__ __launch_bounds__(64 * kWaves) void combine_bwd_kernel(
     const T* __restrict__ dout, const T* __restrict__ y, const int* __restrict__ slot,
     const int* __restrict__ offsets, const void* __restrict__ w, int wdt, int64_t ntok, int K,
@@ -87,6 +131,45 @@ __global__ __launch_bounds__(64 * kWaves) void combine_bwd_kernel(
   const int nvalid = offsets[E];
   const int64_t nw = (int64_t)gridDim.x * kWaves;
   for (int64_t t = (int64_t)blockIdx.x * kWaves + wid; t < ntok; t += nw) {
+    if constexpr (KM > 0) {
+      // dout's chunk once, the KM routed rows' chunks in flight together; the
+      // dot products accumulate per lane in chunk order, as below.
+      int sk[KM];
+      float wk[KM], dot[KM];
+      token_rows<KM>(slot, w, wdt, t, lane, sk, wk);
+#pragma unroll
+      for (int k = 0; k < KM; ++k) dot[k] = 0.f;
+      for (int h0 = lane * N; h0 < H; h0 += 64 * N) {
+        float g[N], v[KM][N];
+        Vec<T>::load(dout + t * H + h0, g);
+#pragma unroll
+        for (int k = 0; k < KM; ++k)
+          if (sk[k] < nvalid) Vec<T>::load(y + (int64_t)sk[k] * H + h0, v[k]);
+#pragma unroll
+        for (int k = 0; k < KM; ++k) {
+          if (sk[k] >= nvalid) continue;
+          float d[N];
+#pragma unroll
+          for (int i = 0; i < N; ++i) {
+            d[i] = g[i] * wk[k];
+            float pr = g[i] * v[k][i];
+            dot[k] += round_prod ? round_bf(pr) : pr;
+          }
+          Vec<T>::store(dy + (int64_t)sk[k] * H + h0, d);
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < KM; ++k) {
+        const float dk = wave_sum(dot[k]);
+        if (lane == 0) {
+          if (wdt == MOE_DTYPE_BF16)
+            ((bf16*)dw)[t * KM + k] = f2bf(dk);
+          else
+            ((float*)dw)[t * KM + k] = dk;
+        }
+      }
+      continue;
+    }
     for (int k = 0; k < K; ++k) {
       const int s = slot[t * K + k];
       const bool valid = s < nvalid;
@@ -117,7 +200,7 @@ __global__ __launch_bounds__(64 * kWaves) void combine_bwd_kernel(
   }
 }
 
-template <typename T>
+template <typename T, int KM>
 __global__ __launch_bounds__(64 * kWaves) void gather_bwd_kernel(
     const T* __restrict__ dxs, const int* __restrict__ slot, const int* __restrict__ offsets,
     const T* __restrict__ addend, int64_t ntok, int K, int E, int H, T* __restrict__ dx) {
@@ -126,17 +209,33 @@ __global__ __launch_bounds__(64 * kWaves) void gather_bwd_kernel(
   const int nvalid = offsets[E];
   const int64_t nw = (int64_t)gridDim.x * kWaves;
   for (int64_t t = (int64_t)blockIdx.x * kWaves + wid; t < ntok; t += nw) {
+    int sk[KM > 0 ? KM : 1];
+    float wk[KM > 0 ? KM : 1];
+    if constexpr (KM > 0) token_rows<KM>(slot, nullptr, 0, t, lane, sk, wk);
     for (int h0 = lane * N; h0 < H; h0 += 64 * N) {
       float acc[N];
 #pragma unroll
       for (int i = 0; i < N; ++i) acc[i] = 0.f;
-      for (int k = 0; k < K; ++k) {
-        const int s = slot[t * K + k];
-        if (s >= nvalid) continue;
-        float v[N];
-        Vec<T>::load(dxs + (int64_t)s * H + h0, v);
+      if constexpr (KM > 0) {
+        float v[KM][N];
 #pragma unroll
-        for (int i = 0; i < N; ++i) acc[i] += v[i];
+        for (int k = 0; k < KM; ++k)
+          if (sk[k] < nvalid) Vec<T>::load(dxs + (int64_t)sk[k] * H + h0, v[k]);
+#pragma unroll
+        for (int k = 0; k < KM; ++k) {
+          if (sk[k] >= nvalid) continue;
+#pragma unroll
+          for (int i = 0; i < N; ++i) acc[i] += v[k][i];
+        }
+      } else {
+        for (int k = 0; k < K; ++k) {
+          const int s = slot[t * K + k];
+          if (s >= nvalid) continue;
+          float v[N];
+          Vec<T>::load(dxs + (int64_t)s * H + h0, v);
+#pragma unroll
+          for (int i = 0; i < N; ++i) acc[i] += v[i];
+        }
       }
       if (addend) {
         // a second gradient of the same tensor: round the sum to T first, as
@@ -168,6 +267,20 @@ int check_rows(int64_t T, int K, int E, int H, int dtype, const char* who) {
 
 bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
+// Launches KERNEL<T, KM> with KM = K for the common top-k values, else the
+// any-K form (KM = 0).
+#define MOE_DISPATCH_K(K, KERNEL, T, ...)                       \
+  do {                                                          \
+    switch (K) {                                                \
+      case 1: KERNEL<T, 1><<<__VA_ARGS__; break;                \
+      case 2: KERNEL<T, 2><<<__VA_ARGS__; break;                \
+      case 4: KERNEL<T, 4><<<__VA_ARGS__; break;                \
+      case 6: KERNEL<T, 6><<<__VA_ARGS__; break;                \
+      case 8: KERNEL<T, 8><<<__VA_ARGS__; break;                \
+      default: KERNEL<T, 0><<<__VA_ARGS__; break;               \
+    }                                                           \
+  } while (0)
+
 }  // namespace
 }  // namespace moe
 
@@ -187,11 +300,11 @@ extern "C" int moe_amd_combine(const void* y, const int32_t* slot, const int32_t
   if (T == 0) return MOE_OK;
   hipStream_t st = (hipStream_t)stream;
   if (dtype == MOE_DTYPE_BF16)
-    combine_kernel<bf16><<<grid_tokens(T), 64 * kWaves, 0, st>>>(
-        (const bf16*)y, slot, offsets, topk_weights, weights_dtype, T, K, E, H, (bf16*)out);
+    MOE_DISPATCH_K(K, combine_kernel, bf16, grid_tokens(T), 64 * kWaves, 0, st>>>(
+        (const bf16*)y, slot, offsets, topk_weights, weights_dtype, T, K, E, H, (bf16*)out));
   else
-    combine_kernel<float><<<grid_tokens(T), 64 * kWaves, 0, st>>>(
-        (const float*)y, slot, offsets, topk_weights, weights_dtype, T, K, E, H, (float*)out);
+    MOE_DISPATCH_K(K, combine_kernel, float, grid_tokens(T), 64 * kWaves, 0, st>>>(
+        (const float*)y, slot, offsets, topk_weights, weights_dtype, T, K, E, H, (float*)out));
   return check_launch(who);
 }
 
@@ -212,13 +325,13 @@ extern "C" int moe_amd_combine_backward(const void* d_out, const void* y, const 
   if (T == 0) return MOE_OK;
   hipStream_t st = (hipStream_t)stream;
   if (dtype == MOE_DTYPE_BF16)
-    combine_bwd_kernel<bf16><<<grid_tokens(T), 64 * kWaves, 0, st>>>(
+    MOE_DISPATCH_K(K, combine_bwd_kernel, bf16, grid_tokens(T), 64 * kWaves, 0, st>>>(
         (const bf16*)d_out, (const bf16*)y, slot, offsets, topk_weights, weights_dtype, T, K, E,
-        H, (bf16*)d_y, d_topk_weights);
+        H, (bf16*)d_y, d_topk_weights));
   else
-    combine_bwd_kernel<float><<<grid_tokens(T), 64 * kWaves, 0, st>>>(
+    MOE_DISPATCH_K(K, combine_bwd_kernel, float, grid_tokens(T), 64 * kWaves, 0, st>>>(
         (const float*)d_out, (const float*)y, slot, offsets, topk_weights, weights_dtype, T, K,
-        E, H, (float*)d_y, d_topk_weights);
+        E, H, (float*)d_y, d_topk_weights));
   return check_launch(who);
 }
 
@@ -234,11 +347,11 @@ int gather_backward_impl(const void* d_xs, const int32_t* slot, const int32_t* o
   if (T == 0) return MOE_OK;
   hipStream_t st = (hipStream_t)stream;
   if (dtype == MOE_DTYPE_BF16)
-    gather_bwd_kernel<bf16><<<grid_tokens(T), 64 * kWaves, 0, st>>>(
-        (const bf16*)d_xs, slot, offsets, (const bf16*)addend, T, K, E, H, (bf16*)d_x);
+    MOE_DISPATCH_K(K, gather_bwd_kernel, bf16, grid_tokens(T), 64 * kWaves, 0, st>>>(
+        (const bf16*)d_xs, slot, offsets, (const bf16*)addend, T, K, E, H, (bf16*)d_x));
   else
-    gather_bwd_kernel<float><<<grid_tokens(T), 64 * kWaves, 0, st>>>(
-        (const float*)d_xs, slot, offsets, (const float*)addend, T, K, E, H, (float*)d_x);
+    MOE_DISPATCH_K(K, gather_bwd_kernel, float, grid_tokens(T), 64 * kWaves, 0, st>>>(
+        (const float*)d_xs, slot, offsets, (const float*)addend, T, K, E, H, (float*)d_x));
   return check_launch(who);
 }
 
