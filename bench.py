@@ -109,12 +109,12 @@ def copy_calibration(nbytes: int) -> None:
 # the same counters on a plain copy of known size (`--copy-calibration`); the
 # commands and per-counter figures are in profiles/gemm_hbm_traffic_L.md.
 RECORDED_TRAFFIC_L = {
-    "gemm_gate_up_swiglu": 12051779536,
-    "gemm_down": 5349018615,
-    "gemm_down_backward_dx_dswiglu": 7894323164,
-    "gemm_gate_up_backward_dx": 8422120319,
-    "gemm_down_backward_dw": 4212811645,
-    "gemm_gate_up_backward_dw": 12081383239,
+    "gemm_gate_up_swiglu": 10026612405,
+    "gemm_down": 5358301900,
+    "gemm_down_backward_dx_dswiglu": 7744586922,
+    "gemm_gate_up_backward_dx": 8175586656,
+    "gemm_down_backward_dw": 3921002086,
+    "gemm_gate_up_backward_dw": 6810623670,
 }
 
 
