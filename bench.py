@@ -3,9 +3,10 @@
 A step is one forward+backward of the whole expert layer over one batch of
 synthetic inputs already resident in HBM: gating linear (MFMA) -> router
 softmax/top-k -> permutation -> grouped GEMM-1 + SwiGLU -> grouped GEMM-2 ->
-combine, then the full backward (combine, GEMM-2 dW, GEMM-2 dX+dSwiGLU,
-GEMM-1 dW, router backward, gating-linear dW (split-K), GEMM-1 dX, gating-
-linear dX, gather + add), every kernel hand-written HIP.  Default
+combine, then the full backward (GEMM-2 dX+dSwiGLU fused with the combine
+backward, routing-weight gradient reduction, GEMM-2 dW, GEMM-1 dW, router
+backward, gating-linear dW (split-K), GEMM-1 dX, gating-linear dX, gather +
+add), every kernel hand-written HIP.  Default
 workload: the L (Qwen3-30B-A3B) layer, T=65536, H=2048, E=128, K=8, I=768,
 bf16.
 
@@ -44,6 +45,8 @@ def gemm_flops(name: str, S: int, H: int, I: int) -> float:
         "moe_amd_gemm_down": 2.0 * S * I * H,
         "moe_amd_gemm_down_backward_dx_dswiglu": 2.0 * S * H * I,
         "moe_amd_gemm_down_backward_dw": 2.0 * S * H * I,
+        "moe_amd_gemm_down_backward_dx_fused": 2.0 * S * H * I,
+        "moe_amd_gemm_down_backward_dw_gathered": 2.0 * S * H * I,
         "moe_amd_gemm_gate_up_backward_dx": 2.0 * S * 2 * I * H,
         "moe_amd_gemm_gate_up_backward_dw": 2.0 * S * 2 * I * H,
     }

@@ -192,6 +192,39 @@ int moe_amd_gemm_down_backward_dw(const void* dy, const void* act, const int32_t
                                   const void* tile_plan, int64_t S, int E, int H, int I,
                                   int dtype, void* d_down_proj, void* stream);
 
+/* The combine's backward fused into GEMM-2's backward, without the [S,H]
+ * d_y = w * d_out[token] of moe_amd_combine_backward: per routed row r of
+ * token t = row_src[r]/K, g = d_out[t] @ down_proj[e] (bf16-rounded);
+ * d_act = w[row_src[r]] * g and (d_gate, d_up) from gate_up as in
+ * moe_amd_gemm_down_backward_dx_dswiglu -> d_gate_up [S,2I];
+ * act_w [S,I] = w * act (act = silu(gate) * up recomputed from gate_up,
+ * bitwise as the forward stored it), the input of
+ * moe_amd_gemm_down_backward_dw_gathered; dw_partials
+ * [T*K][moe_amd_gemm_down_backward_dx_fused_parts(I)] fp32: per column
+ * tile, <g, act> over its columns = that tile's share of
+ * d_w[t,k] = <d_out[t], y[r]>, reduced by moe_amd_weight_grad_reduce.
+ * topk_weights [T*K] in weights_dtype (fp32 or bf16).  Replaces the
+ * autograd of transformers/integrations/moe.py:457-478 (weights multiply,
+ * index_add) and of the down projection :449-459 (formula :226-242). */
+int moe_amd_gemm_down_backward_dx_fused_parts(int I);
+int moe_amd_gemm_down_backward_dx_fused(const void* d_out, const int32_t* row_src, int top_k,
+                                        const int32_t* offsets, const void* tile_plan,
+                                        const void* down_proj, const void* gate_up,
+                                        const void* topk_weights, int weights_dtype, int64_t T,
+                                        int64_t S, int E, int H, int I, int dtype,
+                                        void* d_gate_up, void* act_w, float* dw_partials,
+                                        void* stream);
+
+/* d_down_proj[e] = sum over e's rows r of d_out[row_src[r]/K]^T act_w[r]
+ * ([E,H,I]; zero for empty experts), d_out rows gathered through row_src:
+ * with act_w = w * act this equals moe_amd_gemm_down_backward_dw on
+ * d_y = w * d_out[token].  Tile plan as for moe_amd_gemm_down_backward_dw. */
+int moe_amd_gemm_down_backward_dw_gathered(const void* d_out, const void* act_w,
+                                           const int32_t* row_src, int top_k,
+                                           const int32_t* offsets, const void* tile_plan,
+                                           int64_t T, int64_t S, int E, int H, int I, int dtype,
+                                           void* d_down_proj, void* stream);
+
 /* d_xs = d_gate_up @ gate_up_proj[e]  ([S,H]). */
 int moe_amd_gemm_gate_up_backward_dx(const void* d_gate_up, const int32_t* offsets,
                                      const void* tile_plan, const void* gate_up_proj,
@@ -222,6 +255,14 @@ int moe_amd_combine_backward(const void* d_out, const void* y, const int32_t* sl
                              const int32_t* offsets, const void* topk_weights,
                              int weights_dtype, int64_t T, int K, int E, int H, int dtype,
                              void* d_y, void* d_topk_weights, void* stream);
+
+/* d_topk_weights[i] = sum over c < n_part of partials[i*n_part + c] (fp32
+ * in c order, rounded once to weights_dtype) for the T*K routed entries; 0
+ * where slot[i] is a sentinel row.  The last step of the fused combine
+ * backward (moe_amd_gemm_down_backward_dx_fused). */
+int moe_amd_weight_grad_reduce(const float* partials, int n_part, const int32_t* slot,
+                               const int32_t* offsets, int64_t T, int K, int E,
+                               void* d_topk_weights, int weights_dtype, void* stream);
 
 /* Backward of the gather xs = hidden_states[row_src // K]:
  * d_x[t] = sum_k d_xs[slot[t*K+k]] (fp32 accumulation, sentinels skipped). */

@@ -55,12 +55,18 @@ SIGNATURES: dict[str, tuple] = {
     "moe_amd_gemm_down_backward_dx_dswiglu": (
         _i, [_p, _p, _p, _p, _p, _i64, _i, _i, _i, _i, _p, _p]),
     "moe_amd_gemm_down_backward_dw": (_i, [_p, _p, _p, _p, _i64, _i, _i, _i, _i, _p, _p]),
+    "moe_amd_gemm_down_backward_dx_fused_parts": (_i, [_i]),
+    "moe_amd_gemm_down_backward_dx_fused": (
+        _i, [_p, _p, _i, _p, _p, _p, _p, _p, _i, _i64, _i64, _i, _i, _i, _i, _p, _p, _p, _p]),
+    "moe_amd_gemm_down_backward_dw_gathered": (
+        _i, [_p, _p, _p, _i, _p, _p, _i64, _i64, _i, _i, _i, _i, _p, _p]),
     "moe_amd_gemm_gate_up_backward_dx": (_i, [_p, _p, _p, _p, _i64, _i, _i, _i, _i, _p, _p]),
     "moe_amd_gemm_gate_up_backward_dw": (
         _i, [_p, _p, _p, _i, _p, _p, _i64, _i64, _i, _i, _i, _i, _p, _p]),
     "moe_amd_combine": (_i, [_p, _p, _p, _p, _i, _i64, _i, _i, _i, _i, _p, _p]),
     "moe_amd_combine_backward": (
         _i, [_p, _p, _p, _p, _p, _i, _i64, _i, _i, _i, _i, _p, _p, _p]),
+    "moe_amd_weight_grad_reduce": (_i, [_p, _i, _p, _p, _i64, _i, _i, _p, _i, _p]),
     "moe_amd_gather_backward": (_i, [_p, _p, _p, _i64, _i, _i, _i, _i, _p, _p]),
     "moe_amd_gather_backward_add": (_i, [_p, _p, _p, _p, _i64, _i, _i, _i, _i, _p, _p]),
     "moe_amd_topk_stats_workspace_size": (_sz, [_i64, _i]),

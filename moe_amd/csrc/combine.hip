@@ -281,6 +281,25 @@ bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
     }                                                           \
   } while (0)
 
+// d_w[i] = sum over c < n_part of partials[i * n_part + c] (fp32, in c
+// order), rounded once to the weights' dtype; 0 for sentinel entries (slot
+// past the real experts' rows), which no GEMM tile covers.
+__global__ __launch_bounds__(256) void weight_grad_reduce_kernel(
+    const float* __restrict__ part, int n_part, const int* __restrict__ slot,
+    const int* __restrict__ offsets, int E, int64_t n, void* __restrict__ out, int out_bf16) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  float acc = 0.f;
+  if (slot[i] < offsets[E]) {
+    const float* pp = part + i * n_part;
+    for (int c = 0; c < n_part; ++c) acc += pp[c];
+  }
+  if (out_bf16)
+    ((bf16*)out)[i] = f2bf(acc);
+  else
+    ((float*)out)[i] = acc;
+}
+
 }  // namespace
 }  // namespace moe
 
@@ -369,4 +388,20 @@ extern "C" int moe_amd_gather_backward_add(const void* d_xs, const int32_t* slot
   MOE_REQUIRE(addend, MOE_ERR_ARG, "gather_backward_add: null addend");
   return gather_backward_impl(d_xs, slot, offsets, addend, T, K, E, H, dtype, d_x, stream,
                               "gather_backward_add");
+}
+
+extern "C" int moe_amd_weight_grad_reduce(const float* partials, int n_part, const int32_t* slot,
+                                          const int32_t* offsets, int64_t T, int K, int E,
+                                          void* d_topk_weights, int weights_dtype, void* stream) {
+  const char* who = "weight_grad_reduce";
+  MOE_REQUIRE(T >= 0 && K >= 1 && E >= 1 && n_part >= 1, MOE_ERR_ARG, "%s: bad sizes", who);
+  MOE_REQUIRE(weights_dtype == MOE_DTYPE_F32 || weights_dtype == MOE_DTYPE_BF16, MOE_ERR_ARG,
+              "%s: weights_dtype must be fp32 or bf16", who);
+  MOE_REQUIRE(offsets && (T == 0 || (partials && slot && d_topk_weights)), MOE_ERR_ARG,
+              "%s: null pointer", who);
+  const int64_t n = T * K;
+  if (n == 0) return MOE_OK;
+  weight_grad_reduce_kernel<<<(unsigned)((n + 255) / 256), 256, 0, (hipStream_t)stream>>>(
+      partials, n_part, slot, offsets, E, n, d_topk_weights, weights_dtype == MOE_DTYPE_BF16);
+  return check_launch(who);
 }

@@ -73,19 +73,29 @@ constexpr int SROW = 260;  // bf16 per row of the epilogue staging tile (520 B: 
 // RDX: its input gradient, d_x[T, H] = d_logits[T, E] . W_r[E, H].
 // RDW: its weight gradient split over token chunks c (split-K), fp32
 //      partial[c][E][H] = sum_{t in chunk c} d_logits[t, :]^T x[t, :].
-enum Mode { G1F = 0, G2F = 1, G2DX = 2, G1DX = 3, G2DW = 4, G1DW = 5, RL = 6, RDX = 7, RDW = 8 };
+// G2DXF and G2DWG are the down GEMMs' backward fused with the combine's
+// backward: their row operand is d_out gathered through row_src instead of a
+// materialised d_y = w * d_out[token].  G2DXF also scales by the routing
+// weight, produces the weight gradient and w * act in its epilogue; G2DWG
+// computes d_down_proj[e]^T = (w act)^T d_out[tokens] and stores it
+// transposed.
+enum Mode { G1F = 0, G2F = 1, G2DX = 2, G1DX = 3, G2DW = 4, G1DW = 5, RL = 6, RDX = 7, RDW = 8,
+            G2DXF = 9, G2DWG = 10 };
 
 struct GemmArgs {
   const bf16* x;         // hidden_states [T,H]
   const bf16* w;         // gate_up_proj [E,2I,H] or down_proj [E,H,I]
   const bf16* a0;        // act [S,I] (G2F) | dy [S,H] (G2DX,G2DW) | d_gate_up [S,2I] (G1DX,G1DW)
-  const bf16* a1;        // act [S,I] (G2DW) | gate_up [S,2I] (G2DX)
+  const bf16* a1;        // act [S,I] (G2DW) | gate_up [S,2I] (G2DX, G2DXF)
   const int* row_src;    // [S]
   const int* offsets;    // [E+1]
   const int* tile_count; // token modes: number of row tiles (tile_starts[E] for BR)
   const int4* tile_info; // token modes: {expert, first row, end row, 0} per row tile
   bf16* out;
-  bf16* out2;            // gate_up output of G1F (may be null)
+  bf16* out2;            // gate_up output of G1F (may be null); w * act [S,I] of G2DXF
+  const void* rw;        // G2DXF: routing weights [T*K], fp32 or bf16 (rw_bf16)
+  int rw_bf16;
+  float* dw_part;        // G2DXF: weight-gradient partials [T*K][n_ct] fp32
   float* out_f32;        // RL: fp32 logits (null: bf16 logits in out); RDW: fp32 partials
   int chunk_rows;        // RDW: tokens per split-K chunk
   int64_t T, S;
@@ -157,6 +167,26 @@ __device__ __forceinline__ int div_topk(int n, uint32_t m, int shift) {
   return (int)(((uint64_t)(uint32_t)n * m) >> shift);
 }
 
+// Sum over each 32-lane half of the wave, returned in every lane of that
+// half, in a fixed order: DPP within rows of 16 (quad xor 1, quad xor 2,
+// half-row mirror, row mirror), then the two rows' totals by v_readlane.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float half_wave_sum(float v) {
+  v += dpp_f<0xB1>(v);
+  v += dpp_f<0x4E>(v);
+  v += dpp_f<0x141>(v);
+  v += dpp_f<0x140>(v);
+  const int iv = __float_as_int(v);
+  const float s0 = __int_as_float(__builtin_amdgcn_readlane(iv, 0)) +
+                   __int_as_float(__builtin_amdgcn_readlane(iv, 16));
+  const float s1 = __int_as_float(__builtin_amdgcn_readlane(iv, 32)) +
+                   __int_as_float(__builtin_amdgcn_readlane(iv, 48));
+  return (threadIdx.x & 32) ? s1 : s0;
+}
+
 // Logistic sigmoid from the hardware base-2 exponential and reciprocal
 // (v_exp_f32, v_rcp_f32; about 1 ulp each): 1 / (1 + 2^(-x log2 e)).  The
 // epilogues evaluate it once per output element, where an IEEE expf and
@@ -171,16 +201,21 @@ template <int MODE, int BR>
 __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmArgs p) {
   constexpr int NW = kWaves<BR>;                          // waves, as NW/2 rows x 2 columns
   constexpr int NTHR = NW * 64;
-  constexpr bool TOKEN = MODE <= G1DX;                    // rows = routed rows of one expert
+  constexpr bool TOKEN = MODE <= G1DX || MODE == G2DXF;   // rows = routed rows of one expert
   constexpr bool DENSE = MODE == RL || MODE == RDX;       // rows = all T tokens, one "expert"
   constexpr bool COL_KM = !(MODE == G1F || MODE == G2F || MODE == RL);  // column operand k-major
   constexpr bool ROW_KM = !TOKEN && !DENSE;               // row operand k-major (dW)
+  constexpr bool DOWN_DX = MODE == G2DX || MODE == G2DXF;  // column operand down_proj[e], k-major
+  constexpr bool GROW = MODE == G1F || MODE == G2DXF;      // row operand: token rows via row_src
+  constexpr bool GCOL = MODE == G1DW || MODE == G2DWG;     // column operand: token rows via row_src (k-major)
+  constexpr bool DW = MODE == G2DW || MODE == G1DW || MODE == G2DWG;
+  constexpr bool SWAP = MODE == G2DWG;  // MFMA operands swapped: lanes hold 4 consecutive rows
   constexpr int WR = BR / (NW / 2);                       // rows per wave
   constexpr int TJ = WR / 32;                             // MFMA row sub-tiles per wave
   constexpr int TI = 4;                                   // MFMA col sub-tiles per wave (128 cols)
   constexpr int CPW = BC * BK * 2 / 1024 / NW;            // 1 KB DMA blocks per wave, column half
   constexpr int RPW = BR * BK * 2 / 1024 / NW;            // ... row half
-  constexpr int NTOK = (MODE == G1DW) ? CPW : 0;          // gathered-row indices per lane and stage
+  constexpr int NTOK = GCOL ? CPW : 0;                    // gathered-row indices per lane and stage
   constexpr int NOPS = NTOK + RPW + CPW;                  // memory ops per main-loop step
   constexpr int NGRP = (BK / 16) * TI;                    // MFMA groups per step
   static_assert(CPW * NW == 32 && RPW * NW * 8 == BR && TJ >= 1, "DMA blocks per wave");
@@ -204,7 +239,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
   // their own is exhausted.  Every workgroup stops when all 8 are.
   const int n_tiles = TOKEN ? (*p.tile_count) * p.n_ct : p.n_tiles;
   const int xcd = blockIdx.x & 7, nslot = gridDim.x >> 3;
-  const bool dyn = (MODE == G2DW || MODE == G1DW) && p.queue != nullptr;
+  const bool dyn = DW && p.queue != nullptr;
   const int per_e = p.n_rt * p.n_ct;
   auto claim = [&]() -> int {
     int* box = (int*)smem;  // free: the previous tile's epilogue ended with a barrier
@@ -275,7 +310,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
     d.kbeg = __builtin_amdgcn_readfirstlane(d.kbeg);
     d.kend = __builtin_amdgcn_readfirstlane(d.kend);
     int K_len;
-    if constexpr (MODE == G1F || MODE == G2DX || MODE == RL) K_len = H;
+    if constexpr (MODE == G1F || DOWN_DX || MODE == RL) K_len = H;
     else if constexpr (MODE == RDX) K_len = p.E;
     else if constexpr (MODE == G2F) K_len = I;
     else if constexpr (MODE == G1DX) K_len = I2;
@@ -312,6 +347,8 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
     return make_rsrc(ptr + adv, left);
   };
   int kb_cur = 0, ke_cur = 0;
+  int erow_src = 0;        // G2DXF: row_src of tile row tid
+  uint32_t erow_wraw = 0;  // ... and its routing weight's bits (fp32, or bf16 zero-extended)
 
   auto setup = [&](const Tile& d) {
     kb_cur = d.kbeg;
@@ -344,7 +381,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
     } else {
       // k-major column operand: rows of k, features contiguous.
       int ld;
-      if constexpr (MODE == G2DX) {
+      if constexpr (DOWN_DX) {
         cptr = (const char*)(p.w + (int64_t)d.e * H * I);
         cbytes = (uint32_t)(H * I * 2);
         ld = I;
@@ -364,7 +401,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
         cptr = (const char*)(p.x + (int64_t)d.kbeg * H);
         cbytes = (uint32_t)((int64_t)(d.kend - d.kbeg) * H * 2);
         ld = H;
-      } else {  // G1DW: rows of hidden_states gathered through row_src
+      } else {  // G1DW, G2DWG: rows of hidden_states / d_out gathered through row_src
         cptr = (const char*)p.x;
         cbytes = (uint32_t)(p.T * H * 2);
         ld = H;
@@ -373,12 +410,12 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       for (int i = 0; i < CPW; ++i) {
         const int k = km_krow(wid + NW * i);
         const uint32_t fb = (uint32_t)(d.ct * BC + km_chunk(k) * 8) * 2;
-        coff[i] = (MODE == G1DW) ? fb : (uint32_t)k * (uint32_t)(ld * 2) + fb;
+        coff[i] = GCOL ? fb : (uint32_t)k * (uint32_t)(ld * 2) + fb;
       }
-      cstep = (MODE == G1DW) ? 0 : (uint32_t)BK * ld * 2;
+      cstep = GCOL ? 0 : (uint32_t)BK * ld * 2;
     }
     // Row operand.
-    if constexpr (MODE == G1F) {
+    if constexpr (GROW) {  // hidden_states (G1F) or d_out (G2DXF) rows of the routed tokens
       rptr = (const char*)p.x;
       rbytes = (uint32_t)(p.T * H * 2);
 #pragma unroll
@@ -401,7 +438,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       }
       rstep = BK * 2;
     } else {
-      const int ld = (MODE == G2DW) ? H : (MODE == RDW ? p.E : I2);
+      const int ld = (MODE == G2DW) ? H : (MODE == RDW ? p.E : (MODE == G2DWG ? I : I2));
       rptr = (const char*)(p.a0 + (int64_t)d.kbeg * ld);
       rbytes = (uint32_t)((int64_t)(d.kend - d.kbeg) * ld * 2);
 #pragma unroll
@@ -411,14 +448,18 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       }
       rstep = (uint32_t)BK * ld * 2;
     }
-    if constexpr (MODE == G1DW) isrc = make_rsrc(p.row_src, (uint32_t)(p.S * 4));
+    if constexpr (GCOL) isrc = make_rsrc(p.row_src, (uint32_t)(p.S * 4));
+    // G2DXF: row_src of tile row tid, consumed by the epilogue (the load
+    // completes under the main loop).
+    if constexpr (MODE == G2DXF)
+      if (tid < BR) erow_src = p.row_src[min(d.row0 + tid, d.row_end - 1)];
   };
 
-  // G1DW: raw row_src entries of stage s (one per column block of this
-  // lane).  Reads past S return zero; rows past the expert's range are
+  // G1DW, G2DWG: raw row_src entries of stage s (one per column block of
+  // this lane).  Reads past S return zero; rows past the expert's range are
   // masked when the DMA offsets are formed.
   auto fetch_tok = [&](int s, int (&tk)[NTOK > 0 ? NTOK : 1]) {
-    if constexpr (MODE == G1DW) {
+    if constexpr (GCOL) {
 #pragma unroll
       for (int i = 0; i < NTOK; ++i) {
         const int kr = s * BK + km_krow(wid + NW * i);
@@ -431,7 +472,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
 
   // DMA of the column half of stage s (ring position 2s).
   auto col_off = [&](int s, int i, const int (&tk)[NTOK > 0 ? NTOK : 1]) -> uint32_t {
-    if constexpr (MODE == G1DW) {
+    if constexpr (GCOL) {
       const int kr = s * BK + km_krow(wid + NW * i);
       // Branch-free select (rows past the expert's range read zeros).
       const uint32_t v = (uint32_t)div_topk(tk[i], p.tok_mul, p.tok_shift) * (uint32_t)(H * 2) + coff[i];
@@ -512,6 +553,13 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
   };
 
   f32x16 acc[TI][TJ];
+  // acc[i][j] += column fragment i x row fragment j.  Register 4q+c of a
+  // lane then holds (row l32, column 8q+4hl+c) of the 32x32 sub-tile, or,
+  // with the operands swapped, (row 8q+4hl+c, column l32).
+  auto mma = [](const bf16x8& a, const bf16x8& b, const f32x16& c) {
+    if constexpr (SWAP) return __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, a, c, 0, 0, 0);
+    else return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  };
 
   for (; dyn ? t >= 0 : t < t_end; t = dyn ? claim() : t + nslot) {
     const Tile cur = decode(t);
@@ -551,10 +599,19 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       issue_row(0);
       __builtin_amdgcn_sched_barrier(0);
       issue_col(1, tk_b);
+      if constexpr (MODE == G2DXF) {
+        // The row's routing weight, in flight under the main loop (raw bits:
+        // converting here would wait for the load).  Being the youngest op,
+        // it makes the first stage wait cover one more column block, which
+        // only strengthens it.
+        if (tid < BR)
+          erow_wraw = p.rw_bf16 ? (uint32_t)((const uint16_t*)p.rw)[erow_src]
+                                : ((const uint32_t*)p.rw)[erow_src];
+      }
       // Op o of window W(w); `tk` holds the row_src entries of stage w+2.
       auto win_op = [&](int w, int o, const int (&tk)[NTOK > 0 ? NTOK : 1]) {
         if (o < NTOK) {
-          if constexpr (MODE == G1DW) {
+          if constexpr (GCOL) {
             const int kr = (w + 3) * BK + km_krow(wid + NW * o);
             tn[o] = __builtin_amdgcn_raw_buffer_load_b32(isrc, (uint32_t)(kb_cur + kr) * 4, 0, 0);
           }
@@ -606,8 +663,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
             if (i < TJ) fb[(ks + 1) & 1][i] = read_b(ks + 1, i);
 #pragma unroll
             for (int j = 0; j < TJ; ++j)
-              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[ks & 1][i], fb[ks & 1][j],
-                                                                  acc[i][j], 0, 0, 0);
+              acc[i][j] = mma(fa[ks & 1][i], fb[ks & 1][j], acc[i][j]);
             group_order();
             __builtin_amdgcn_sched_barrier(0);
           }
@@ -635,7 +691,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
           if (i < TJ) fb[0][i] = read_b(0, i);
 #pragma unroll
           for (int j = 0; j < TJ; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[1][i], fb[1][j], acc[i][j], 0, 0, 0);
+            acc[i][j] = mma(fa[1][i], fb[1][j], acc[i][j]);
           group_order();
           __builtin_amdgcn_sched_barrier(0);
         }
@@ -678,12 +734,29 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       for (int i = 0; i < TI; ++i)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const int row = wr * WR + j * 32 + l32;
-          const int col = wc * 128 + i * 32 + 8 * q + 4 * hl;
           u32x2 v = {pack_bf2(acc[i][j][4 * q + 0], acc[i][j][4 * q + 1]),
                      pack_bf2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3])};
-          *(u32x2*)(stg + row * SROW + col) = v;
+          if constexpr (SWAP) {
+            // four consecutive tile rows of one column: staged transposed,
+            // [column][row], so the store below writes C^T row by row
+            const int col = wc * 128 + i * 32 + l32;
+            const int row = wr * WR + j * 32 + 8 * q + 4 * hl;
+            *(u32x2*)(stg + col * SROW + row) = v;
+          } else {
+            const int row = wr * WR + j * 32 + l32;
+            const int col = wc * 128 + i * 32 + 8 * q + 4 * hl;
+            *(u32x2*)(stg + row * SROW + col) = v;
+          }
         }
+    // G2DXF: each tile row's routing weight and row_src, past the staging tile.
+    float* const erow_w = (float*)(stg + BR * SROW);
+    int* const erow_s = (int*)(erow_w + BR);
+    if constexpr (MODE == G2DXF) {
+      if (tid < BR) {
+        erow_w[tid] = __uint_as_float(p.rw_bf16 ? erow_wraw << 16 : erow_wraw);
+        erow_s[tid] = erow_src;
+      }
+    }
     __syncthreads();
     if constexpr (MODE == G1F) {
       // 128 output features per tile; 16 lanes x 8 features per row, in
@@ -724,14 +797,19 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
           }
         }
       }
-    } else if constexpr (MODE == G2DX) {
+    } else if constexpr (DOWN_DX) {
       // d_act tile (bf16) -> d_gate, d_up with gate/up read back from gate_up.
+      // G2DXF: the tile holds g = d_out[token] . down_proj[e] instead, and
+      // per row d_act = w * g, the weight gradient's partial g . act over
+      // the tile's columns (act = silu(gate) * up recomputed exactly as the
+      // forward stored it), and w * act for the dW GEMM.
       // Each thread owns NB batches of RB rows; the gate/up loads of batch
       // b+1 are issued before batch b is computed and stored, so loads never
       // queue behind this thread's stores.  Loads are clamped in bounds
       // (rows past the tile's end re-read its last row) and only the stores
       // are predicated.
-      constexpr int RB = 8, NB = BR / (RB * (NTHR / 32));
+      constexpr bool FUSED = MODE == G2DXF;
+      constexpr int RB = FUSED ? 4 : 8, NB = BR / (RB * (NTHR / 32));  // FUSED: ~256 VGPRs
       const int c0 = (tid & 31) * 8;
       const int f = cur.ct * BC + c0;
       const bool fok = f < I;
@@ -755,34 +833,51 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
           const int row = (tid >> 5) + (b * RB + q) * (NTHR / 32);
           const int r = cur.row0 + row;
           const u32x4 dav = *(const u32x4*)(stg + row * SROW + c0);
-          u32x4 dgv, duv;
+          const float wgt = FUSED ? erow_w[row] : 1.f;
+          float dot = 0.f;
+          u32x4 dgv, duv, awv;
 #pragma unroll
           for (int w = 0; w < 4; ++w) {
-            float dg[2], du[2];
+            float dg[2], du[2], aw[2];
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-              const float da = h ? bf_hi(dav[w]) : bf_lo(dav[w]);
+              const float gq = h ? bf_hi(dav[w]) : bf_lo(dav[w]);
               const float g = h ? bf_hi(gv[b & 1][q][w]) : bf_lo(gv[b & 1][q][w]);
               const float u = h ? bf_hi(uv[b & 1][q][w]) : bf_lo(uv[b & 1][q][w]);
               const float sg = fast_sigmoid(g);
               const float sl = round_bf(g * sg);          // silu(g) as stored in bf16
+              const float da = FUSED ? wgt * gq : gq;
               const float ds = round_bf(da * u);          // d silu(g)
               du[h] = da * sl;
               dg[h] = ds * (sg * (1.f + g * (1.f - sg)));
+              if constexpr (FUSED) {
+                const float a = round_bf(sl * u);         // act as the forward stored it
+                dot += gq * a;
+                aw[h] = wgt * a;
+              }
             }
             dgv[w] = pack_bf2(dg[0], dg[1]);
             duv[w] = pack_bf2(du[0], du[1]);
+            if constexpr (FUSED) awv[w] = pack_bf2(aw[0], aw[1]);
+          }
+          if constexpr (FUSED) {
+            // Sum over the row's 32 lanes in a fixed order (deterministic).
+            const float tot = half_wave_sum(fok ? dot : 0.f);
+            if ((lane & 31) == 0 && r < cur.row_end)
+              p.dw_part[(int64_t)erow_s[row] * p.n_ct + cur.ct] = tot;
           }
           if (r < cur.row_end && fok) {
             *(u32x4*)(p.out + (int64_t)r * I2 + f) = dgv;
             *(u32x4*)(p.out + (int64_t)r * I2 + I + f) = duv;
+            if constexpr (FUSED) *(u32x4*)(p.out2 + (int64_t)r * I + f) = awv;
           }
         }
       }
     } else {
-      // Plain bf16 tile: y (G2F), d_xs (G1DX), d_down_proj (G2DW), d_gate_up_proj (G1DW).
+      // Plain bf16 tile: y (G2F), d_xs (G1DX), d_down_proj (G2DW, G2DWG
+      // from its transposed staging), d_gate_up_proj (G1DW).
       const int c0 = (tid & 31) * 8;
-      const int f = cur.ct * BC + c0;
+      const int f = (SWAP ? cur.row0 : cur.ct * BC) + c0;
       int nrows, ld;
       bf16* obase;
       if constexpr (TOKEN) {
@@ -794,9 +889,10 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
         ld = MODE == RL ? p.E : H;
         obase = p.out;
       } else {
-        nrows = (MODE == G2DW) ? H : I2;
-        ld = (MODE == G2DW) ? I : H;
-        obase = p.out + (int64_t)cur.e * (MODE == G2DW ? (int64_t)H * I : (int64_t)I2 * H);
+        constexpr bool DOWN = MODE == G2DW || MODE == G2DWG;
+        nrows = DOWN ? H : I2;
+        ld = DOWN ? I : H;
+        obase = p.out + (int64_t)cur.e * (DOWN ? (int64_t)H * I : (int64_t)I2 * H);
       }
       // Batches of RB rows: all LDS reads of a batch first, then its stores,
       // so the LDS latency is paid once per batch rather than per row.
@@ -815,7 +911,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
 #pragma unroll
         for (int q = 0; q < RB; ++q) {
           const int row = (tid >> 5) + (b * RB + q) * (NTHR / 32);
-          const int r = cur.row0 + row;
+          const int r = (SWAP ? cur.ct * BC : cur.row0) + row;
           if (r < nrows && fok) *(u32x4*)(obase + (int64_t)r * ld + f) = v[q];
         }
       }
@@ -855,7 +951,8 @@ int num_cus() {
 template <int MODE, int BR>
 int launch(const GemmArgs& a, int max_tiles, hipStream_t st) {
   constexpr size_t stages = (size_t)NSLOT * SLOT;
-  constexpr size_t staging = (size_t)BR * SROW * sizeof(bf16);
+  // staging tile, plus G2DXF's per-row weights and row_src
+  constexpr size_t staging = (size_t)BR * SROW * sizeof(bf16) + (MODE == G2DXF ? (size_t)BR * 8 : 0);
   const size_t lds = stages > staging ? stages : staging;
   if (max_tiles <= 0) return MOE_OK;
   hipError_t err = hipFuncSetAttribute((const void*)grouped_gemm_kernel<MODE, BR>,
@@ -1133,6 +1230,45 @@ extern "C" int moe_amd_gemm_down_backward_dx_dswiglu(const void* dy, const int32
   return launch_token<G2DX>(a, S, E, BC, I, tile_plan, (hipStream_t)stream);
 }
 
+extern "C" int moe_amd_gemm_down_backward_dx_fused_parts(int I) { return (I + BC - 1) / BC; }
+
+extern "C" int moe_amd_gemm_down_backward_dx_fused(
+    const void* d_out, const int32_t* row_src, int top_k, const int32_t* offsets,
+    const void* tile_plan, const void* down_proj, const void* gate_up, const void* topk_weights,
+    int weights_dtype, int64_t T, int64_t S, int E, int H, int I, int dtype, void* d_gate_up,
+    void* act_w, float* dw_partials, void* stream) {
+  const char* who = "gemm_down_backward_dx_fused";
+  int rc = check_common(S, E, H, I, dtype, who);
+  if (rc) return rc;
+  MOE_REQUIRE(top_k >= 1 && S == T * top_k, MOE_ERR_ARG, "%s: S != T*top_k", who);
+  MOE_REQUIRE(T * (int64_t)H * 2 < ((int64_t)1 << 31), MOE_ERR_UNSUPPORTED, "%s: T*H too large",
+              who);
+  MOE_REQUIRE(weights_dtype == MOE_DTYPE_F32 || weights_dtype == MOE_DTYPE_BF16, MOE_ERR_ARG,
+              "%s: weights_dtype must be fp32 or bf16", who);
+  MOE_REQUIRE(d_out && row_src && offsets && tile_plan && down_proj && gate_up && topk_weights &&
+                  d_gate_up && act_w && dw_partials,
+              MOE_ERR_ARG, "%s: null pointer", who);
+  MOE_ALIGNED(d_out, who);
+  MOE_ALIGNED(down_proj, who);
+  MOE_ALIGNED(gate_up, who);
+  MOE_ALIGNED(d_gate_up, who);
+  MOE_ALIGNED(act_w, who);
+  if (S == 0) return MOE_OK;
+  GemmArgs a{};
+  a.x = (const bf16*)d_out;
+  a.w = (const bf16*)down_proj;
+  a.a1 = (const bf16*)gate_up;
+  a.row_src = row_src;
+  a.offsets = offsets;
+  a.out = (bf16*)d_gate_up;
+  a.out2 = (bf16*)act_w;
+  a.rw = topk_weights;
+  a.rw_bf16 = weights_dtype == MOE_DTYPE_BF16;
+  a.dw_part = dw_partials;
+  a.T = T; a.S = S; a.E = E; a.H = H; a.I = I; set_topk(a, top_k);
+  return launch_token<G2DXF>(a, S, E, BC, I, tile_plan, (hipStream_t)stream);
+}
+
 extern "C" int moe_amd_gemm_gate_up_backward_dx(const void* d_gate_up, const int32_t* offsets,
                                                 const void* tile_plan,
                                                 const void* gate_up_proj, int64_t S, int E,
@@ -1191,6 +1327,40 @@ extern "C" int moe_amd_gemm_down_backward_dw(const void* dy, const void* act,
   a.n_tiles = E * a.n_rt * a.n_ct;
   set_dw_schedule(a, tile_plan, S, E, 0);
   return launch<G2DW, 256>(a, a.n_tiles, (hipStream_t)stream);
+}
+
+extern "C" int moe_amd_gemm_down_backward_dw_gathered(const void* d_out, const void* act_w,
+                                                      const int32_t* row_src, int top_k,
+                                                      const int32_t* offsets,
+                                                      const void* tile_plan, int64_t T, int64_t S,
+                                                      int E, int H, int I, int dtype,
+                                                      void* d_down_proj, void* stream) {
+  const char* who = "gemm_down_backward_dw_gathered";
+  int rc = check_common(S, E, H, I, dtype, who);
+  if (rc) return rc;
+  MOE_REQUIRE(top_k >= 1 && S == T * top_k, MOE_ERR_ARG, "%s: S != T*top_k", who);
+  MOE_REQUIRE(T * (int64_t)H * 2 < ((int64_t)1 << 31), MOE_ERR_UNSUPPORTED, "%s: T*H too large",
+              who);
+  MOE_REQUIRE((S == 0 || (d_out && act_w && row_src)) && offsets && d_down_proj, MOE_ERR_ARG,
+              "%s: null pointer", who);
+  if (S > 0) {
+    MOE_ALIGNED(d_out, who);
+    MOE_ALIGNED(act_w, who);
+  }
+  MOE_ALIGNED(d_down_proj, who);
+  GemmArgs a{};
+  a.x = (const bf16*)d_out;
+  a.a0 = (const bf16*)act_w;
+  a.row_src = row_src;
+  a.offsets = offsets;
+  a.out = (bf16*)d_down_proj;
+  a.T = T; a.S = S; a.E = E; a.H = H; a.I = I; set_topk(a, top_k);
+  // tiles of d_down_proj[e]^T: I rows x H columns
+  a.n_rt = (I + 255) / 256;
+  a.n_ct = (H + BC - 1) / BC;
+  a.n_tiles = E * a.n_rt * a.n_ct;
+  set_dw_schedule(a, tile_plan, S, E, 0);
+  return launch<G2DWG, 256>(a, a.n_tiles, (hipStream_t)stream);
 }
 
 extern "C" int moe_amd_gemm_gate_up_backward_dw(const void* d_gate_up, const void* hidden_states,

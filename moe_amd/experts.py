@@ -31,20 +31,22 @@ class MoEExpertsFunction(torch.autograd.Function):
         y = ops.gemm_down(act, plan, down_proj)
         out = ops.combine(y, plan, top_k_weights)
         if need_grad:
-            ctx.save_for_backward(hidden_states, top_k_weights, gate_up_proj, down_proj, gu, act, y)
+            # y and act are not kept: the backward recomputes act from gu
+            ctx.save_for_backward(hidden_states, top_k_weights, gate_up_proj, down_proj, gu)
             ctx.plan = plan
         return out
 
     @staticmethod
     def backward(ctx, d_out):
-        x, w, gate_up_proj, down_proj, gu, act, y = ctx.saved_tensors
+        x, w, gate_up_proj, down_proj, gu = ctx.saved_tensors
         plan = ctx.plan
         need_x, _, need_w, need_w1, need_w2 = ctx.needs_input_grad
-        d_out = d_out.to(y.dtype)
-        dy, dw = ops.combine_backward(d_out, y, plan, w)
-        d_w2 = ops.gemm_down_backward_dw(dy, act, plan, down_proj.shape) if need_w2 else None
-        d_gu = ops.gemm_down_backward_dx_dswiglu(dy, plan, down_proj, gu)
-        del dy
+        d_out = d_out.to(x.dtype)
+        # combine backward fused into GEMM-2's backward (no [S,H] d_y)
+        d_gu, act_w, dw = ops.gemm_down_backward_fused(d_out, plan, down_proj, gu, w)
+        d_w2 = (ops.gemm_down_backward_dw_gathered(d_out, act_w, plan, down_proj.shape)
+                if need_w2 else None)
+        del act_w
         d_w1 = (ops.gemm_gate_up_backward_dw(d_gu, x, plan, gate_up_proj.shape)
                 if need_w1 else None)
         d_x = None

@@ -43,22 +43,25 @@ class SoftmaxMoELayerFunction(torch.autograd.Function):
         out = ops.combine(y, plan, w)
         ctx.mark_non_differentiable(idx)
         if need:
-            ctx.save_for_backward(x, w_router, gate_up_proj, down_proj, gu, act, y, probs, w, idx)
+            # y and act are not kept: the backward recomputes act from gu
+            ctx.save_for_backward(x, w_router, gate_up_proj, down_proj, gu, probs, w, idx)
             ctx.plan = plan
             ctx.renormalize = renormalize
         return out, probs, w, idx
 
     @staticmethod
     def backward(ctx, d_out, d_probs, d_w, d_idx):
-        x, w_router, gate_up_proj, down_proj, gu, act, y, probs, w, idx = ctx.saved_tensors
+        x, w_router, gate_up_proj, down_proj, gu, probs, w, idx = ctx.saved_tensors
         plan = ctx.plan
         need_x, need_wr, need_w1, need_w2 = ctx.needs_input_grad[:4]
         if d_out is None:
-            d_out = torch.zeros(x.shape, dtype=y.dtype, device=y.device)
-        dy, dw = ops.combine_backward(d_out.to(y.dtype), y, plan, w)
-        d_w2 = ops.gemm_down_backward_dw(dy, act, plan, down_proj.shape) if need_w2 else None
-        d_gu = ops.gemm_down_backward_dx_dswiglu(dy, plan, down_proj, gu)
-        del dy
+            d_out = torch.zeros(x.shape, dtype=x.dtype, device=x.device)
+        d_out = d_out.to(x.dtype)
+        # combine backward fused into GEMM-2's backward (no [S,H] d_y)
+        d_gu, act_w, dw = ops.gemm_down_backward_fused(d_out, plan, down_proj, gu, w)
+        d_w2 = (ops.gemm_down_backward_dw_gathered(d_out, act_w, plan, down_proj.shape)
+                if need_w2 else None)
+        del act_w
         d_w1 = (ops.gemm_gate_up_backward_dw(d_gu, x, plan, gate_up_proj.shape)
                 if need_w1 else None)
         if d_w is not None:

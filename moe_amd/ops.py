@@ -298,6 +298,52 @@ def gemm_down_backward_dx_dswiglu(dy, plan: RoutingPlan, down_proj, gate_up):
     return dgu
 
 
+def gemm_down_backward_fused(d_out, plan: RoutingPlan, down_proj, gate_up, topk_weights):
+    """Backward of the combine and of GEMM-2 + SwiGLU in one GEMM, without
+    materialising d_y = w * d_out[token] ([S,H]): per routed row, g = d_out[t]
+    . down_proj[e]; d_gate_up from d_act = w * g; the routing-weight gradient
+    <d_out[t], y[r]> = <g, act[r]> (act recomputed from gate_up).  Returns
+    (d_gate_up [S,2I], act_w [S,I] = w * act for gemm_down_backward_dw_gathered,
+    d_topk_weights [T,K] in topk_weights' dtype)."""
+    _need_cuda(d_out, down_proj, gate_up, topk_weights)
+    d_out = _contig(d_out)
+    topk_weights = _contig(topk_weights)
+    E, H, I = down_proj.shape
+    S, T, K = plan.num_rows, plan.num_tokens, plan.top_k
+    dev, dt = d_out.device, d_out.dtype
+    n_part = int(_lib.load().moe_amd_gemm_down_backward_dx_fused_parts(I))
+    dgu = torch.empty(S, 2 * I, device=dev, dtype=dt)
+    act_w = torch.empty(S, I, device=dev, dtype=dt)
+    part = torch.empty(S, n_part, device=dev, dtype=torch.float32)
+    dw = torch.empty(T, K, device=dev, dtype=topk_weights.dtype)
+    st = _stream(d_out)
+    _call("moe_amd_gemm_down_backward_dx_fused", d_out.data_ptr(), plan.row_src.data_ptr(), K,
+          plan.offsets.data_ptr(), plan.tile_plan.data_ptr(), down_proj.data_ptr(),
+          gate_up.data_ptr(), topk_weights.data_ptr(), _dtype_code(topk_weights.dtype), T, S, E,
+          H, I, _dtype_code(dt), dgu.data_ptr(), act_w.data_ptr(), part.data_ptr(), st)
+    _call("moe_amd_weight_grad_reduce", part.data_ptr(), n_part, plan.slot.data_ptr(),
+          plan.offsets.data_ptr(), T, K, E, dw.data_ptr(), _dtype_code(dw.dtype), st)
+    return dgu, act_w, dw
+
+
+def gemm_down_backward_dw_gathered(d_out, act_w, plan: RoutingPlan, down_proj_shape, out=None,
+                                   scheduled: bool = True):
+    """d_down_proj[e] = sum over e's rows r of d_out[token(r)]^T act_w[r]
+    ([E,H,I]) with d_out rows gathered through row_src; the dW GEMM of
+    gemm_down_backward_fused's output.  ``scheduled`` as for
+    gemm_down_backward_dw."""
+    _need_cuda(d_out, act_w)
+    d_out = _contig(d_out)
+    E, H, I = down_proj_shape
+    S = plan.num_rows
+    dw = out if out is not None else torch.empty(E, H, I, device=d_out.device, dtype=d_out.dtype)
+    _call("moe_amd_gemm_down_backward_dw_gathered", d_out.data_ptr(), act_w.data_ptr(),
+          plan.row_src.data_ptr(), plan.top_k, plan.offsets.data_ptr(),
+          plan.tile_plan.data_ptr() if scheduled else None, plan.num_tokens, S, E, H, I,
+          _dtype_code(d_out.dtype), dw.data_ptr(), _stream(d_out))
+    return dw
+
+
 def gemm_down_backward_dw(dy, act, plan: RoutingPlan, down_proj_shape, out=None,
                           scheduled: bool = True):
     """d_down_proj [E,H,I].  ``scheduled``: claim tiles from the plan's dW

@@ -99,6 +99,37 @@ def test_backward_parity(T, H, E, K, I, skew, sent, wdt):
             assert w1s.grad[e].abs().max().item() == 0 and w2s.grad[e].abs().max().item() == 0
 
 
+@pytest.mark.parametrize("T,H,E,K,I,skew,sent,wdt", CASES)
+def test_down_backward_fused_parity(T, H, E, K, I, skew, sent, wdt):
+    """The combine backward fused into GEMM-2's backward (d_out rows gathered
+    by token, no d_y): d_gate_up, the routing-weight gradient and d_down_proj
+    against the oracle (which rounds d_y = w * d_out as the reference does;
+    the fused path rounds g = d_out . down_proj instead, hence the tolerance),
+    and the side output act_w bit-exact to w * act."""
+    print(f"fused down backward T={T} H={H} E={E} K={K} I={I} skew={skew} sent={sent} {wdt}",
+          flush=True)
+    x, idx, w, w1, w2, dout = _inputs(T, H, E, K, I, T + E + 2, skew, sent, wdt)
+    _, cache = O.experts_forward(x, idx, w, w1, w2)
+    _, dw_ref, _, dw2_ref, inter = O.experts_backward(cache, x, w, w1, w2, dout)
+    plan = ops.permute(idx.to(DEV), E)
+    gu, act = ops.gemm_gate_up_swiglu(x.to(DEV), plan, w1.to(DEV))
+    wd, dd = w.to(DEV), dout.to(DEV)
+    d_gu, act_w, dw = ops.gemm_down_backward_fused(dd, plan, w2.to(DEV), gu, wd)
+    d_w2 = ops.gemm_down_backward_dw_gathered(dd, act_w, plan, w2.shape)
+    d_w2s = ops.gemm_down_backward_dw_gathered(dd, act_w, plan, w2.shape, scheduled=False)
+    torch.cuda.synchronize()
+    nv = int(cache["plan"].offsets[E])
+    wrow = wd.reshape(-1)[plan.row_src[:nv].long()].float()
+    assert torch.equal(act_w[:nv], (act[:nv].float() * wrow[:, None]).to(torch.bfloat16))
+    assert dw.dtype == wdt
+    assert _rel(dw, dw_ref) < TOL
+    if sent:
+        assert not dw.cpu()[idx >= E].any()        # sentinel entries: zero gradient
+    assert _rel(d_gu[:nv], inter["d_gate_up"][:nv]) < TOL
+    assert _rel(d_w2, dw2_ref) < TOL
+    assert torch.equal(d_w2, d_w2s)               # claimed and static tile walks agree
+
+
 def test_layer_deterministic_and_drop_in_shapes():
     """Two identical fwd+bwd calls give bitwise-identical results."""
     x, idx, w, w1, w2, dout = _inputs(1536, 512, 32, 4, 256, seed=9)
