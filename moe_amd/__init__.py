@@ -6,14 +6,15 @@ Public API:
   MI355XTopKRouter / MI355XDeepSeekRouter                                     # router modules
   hf.register() / hf.install(model)                                           # transformers hook
   ops.*                                                                       # one wrapper per C entry
+  torch.ops.moe_amd.*                                                         # custom ops (library.py)
 """
-from . import ops
-from .experts import MoEExpertsFunction, experts_forward, mi355x_experts_forward
+from . import library, ops
+from .experts import experts_forward, mi355x_experts_forward
 from .router import MI355XDeepSeekRouter, MI355XTopKRouter
 
 __all__ = [
     "ops",
-    "MoEExpertsFunction",
+    "library",
     "experts_forward",
     "mi355x_experts_forward",
     "MI355XTopKRouter",

@@ -1,8 +1,13 @@
 """The expert layer: permute -> grouped GEMM-1 + SwiGLU -> grouped GEMM-2 ->
 combine, with a hand-written backward, all on the HIP kernels.
 
-``experts_forward`` is the functional form; ``mi355x_experts_forward`` has
-the transformers ExpertsInterface signature
+``experts_forward`` is the functional form, a call of the differentiable
+custom op ``moe_amd::experts_fwd`` (fake and autograd registered, so
+torch.compile traces it without a graph break, as the reference's backend
+registers its grouped GEMM, integrations/moe.py:245-257; backward op
+``moe_amd::experts_bwd``, formulas :226-242, the combine's backward fused
+into GEMM-2's).  ``mi355x_experts_forward`` has the transformers
+ExpertsInterface signature
 ``fn(self, hidden_states [T,H], top_k_index [T,K], top_k_weights [T,K])``
 (transformers/integrations/moe.py:377-382) and reads the bank's
 ``gate_up_proj [E,2I,H]`` / ``down_proj [E,H,I]`` from ``self``.
@@ -11,50 +16,7 @@ from __future__ import annotations
 
 import torch
 
-from . import ops
-
-
-class MoEExpertsFunction(torch.autograd.Function):
-    """Autograd node of one expert-layer call.
-
-    Differentiable w.r.t. hidden_states, top_k_weights, gate_up_proj and
-    down_proj (not top_k_index), as the reference's grouped_mm path is
-    (transformers/integrations/moe.py:377-478; backward formulas :226-242)."""
-
-    @staticmethod
-    def forward(ctx, hidden_states, top_k_index, top_k_weights, gate_up_proj, down_proj):
-        E = gate_up_proj.shape[0]
-        plan = ops.permute(top_k_index, E)
-        need_grad = any(ctx.needs_input_grad)
-        gu, act = ops.gemm_gate_up_swiglu(hidden_states, plan, gate_up_proj,
-                                          save_gate_up=need_grad)
-        y = ops.gemm_down(act, plan, down_proj)
-        out = ops.combine(y, plan, top_k_weights)
-        if need_grad:
-            # y and act are not kept: the backward recomputes act from gu
-            ctx.save_for_backward(hidden_states, top_k_weights, gate_up_proj, down_proj, gu)
-            ctx.plan = plan
-        return out
-
-    @staticmethod
-    def backward(ctx, d_out):
-        x, w, gate_up_proj, down_proj, gu = ctx.saved_tensors
-        plan = ctx.plan
-        need_x, _, need_w, need_w1, need_w2 = ctx.needs_input_grad
-        d_out = d_out.to(x.dtype)
-        # combine backward fused into GEMM-2's backward (no [S,H] d_y)
-        d_gu, act_w, dw = ops.gemm_down_backward_fused(d_out, plan, down_proj, gu, w)
-        d_w2 = (ops.gemm_down_backward_dw_gathered(d_out, act_w, plan, down_proj.shape)
-                if need_w2 else None)
-        del act_w
-        d_w1 = (ops.gemm_gate_up_backward_dw(d_gu, x, plan, gate_up_proj.shape)
-                if need_w1 else None)
-        d_x = None
-        if need_x:
-            d_xs = ops.gemm_gate_up_backward_dx(d_gu, plan, gate_up_proj)
-            d_x = ops.gather_backward(d_xs, plan)
-        ctx.plan = None
-        return d_x, None, (dw if need_w else None), d_w1, d_w2
+from . import library  # noqa: F401  (registers the moe_amd:: ops)
 
 
 def experts_forward(hidden_states: torch.Tensor, top_k_index: torch.Tensor,
@@ -78,8 +40,11 @@ def experts_forward(hidden_states: torch.Tensor, top_k_index: torch.Tensor,
         raise ValueError("top_k_index / top_k_weights must both be [T, K]")
     out_dtype = hidden_states.dtype
     x = hidden_states.to(gate_up_proj.dtype).contiguous()
-    out = MoEExpertsFunction.apply(x, top_k_index, top_k_weights.contiguous(),
-                                   gate_up_proj.contiguous(), down_proj.contiguous())
+    w = top_k_weights.contiguous()
+    save = torch.is_grad_enabled() and any(t.requires_grad
+                                           for t in (x, w, gate_up_proj, down_proj))
+    out = torch.ops.moe_amd.experts_fwd(x, top_k_index, w, gate_up_proj.contiguous(),
+                                        down_proj.contiguous(), save)[0]
     return out.to(out_dtype)
 
 

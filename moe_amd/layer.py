@@ -12,75 +12,9 @@ from __future__ import annotations
 import torch
 from torch import nn
 
-from . import ops
+from . import library  # noqa: F401  (registers the moe_amd:: ops)
 from .experts import experts_forward
-from .router import SigmoidTopKFunction, SoftmaxTopKFunction, gating_linear
-
-
-class SoftmaxMoELayerFunction(torch.autograd.Function):
-    """Gating linear + softmax router + experts as ONE autograd node, so that
-    the two gradients of the hidden states (through the gating linear and
-    through the experts) meet inside the gather backward
-    (``gather_backward(..., addend=router dx)``) instead of in autograd's
-    separate add, and the gating linear's dX runs on the MFMA kernel.  The
-    arithmetic is that of the composed path (RouterLinearFunction,
-    SoftmaxTopKFunction, MoEExpertsFunction): every rounding point is kept,
-    only the fp32 summation orders of the two router GEMMs differ.
-
-    Inputs: x [T,H] bf16, w_router [E,H] bf16, gate_up_proj, down_proj (bf16).
-    Outputs: (out [T,H], probs [T,E] fp32, weights [T,K] fp32, index [T,K])."""
-
-    @staticmethod
-    def forward(ctx, x, w_router, gate_up_proj, down_proj, top_k, renormalize, logit_offset):
-        ctx.set_materialize_grads(False)
-        logits = ops.router_linear(x, w_router, torch.bfloat16)
-        probs, w, idx = ops.router_softmax_topk(logits, top_k, renormalize, logit_offset)
-        del logits
-        plan = ops.permute(idx, gate_up_proj.shape[0])
-        need = any(ctx.needs_input_grad)
-        gu, act = ops.gemm_gate_up_swiglu(x, plan, gate_up_proj, save_gate_up=need)
-        y = ops.gemm_down(act, plan, down_proj)
-        out = ops.combine(y, plan, w)
-        ctx.mark_non_differentiable(idx)
-        if need:
-            # y and act are not kept: the backward recomputes act from gu
-            ctx.save_for_backward(x, w_router, gate_up_proj, down_proj, gu, probs, w, idx)
-            ctx.plan = plan
-            ctx.renormalize = renormalize
-        return out, probs, w, idx
-
-    @staticmethod
-    def backward(ctx, d_out, d_probs, d_w, d_idx):
-        x, w_router, gate_up_proj, down_proj, gu, probs, w, idx = ctx.saved_tensors
-        plan = ctx.plan
-        need_x, need_wr, need_w1, need_w2 = ctx.needs_input_grad[:4]
-        if d_out is None:
-            d_out = torch.zeros(x.shape, dtype=x.dtype, device=x.device)
-        d_out = d_out.to(x.dtype)
-        # combine backward fused into GEMM-2's backward (no [S,H] d_y)
-        d_gu, act_w, dw = ops.gemm_down_backward_fused(d_out, plan, down_proj, gu, w)
-        d_w2 = (ops.gemm_down_backward_dw_gathered(d_out, act_w, plan, down_proj.shape)
-                if need_w2 else None)
-        del act_w
-        d_w1 = (ops.gemm_gate_up_backward_dw(d_gu, x, plan, gate_up_proj.shape)
-                if need_w1 else None)
-        if d_w is not None:
-            dw = dw + d_w.float()
-        d_logits = ops.router_softmax_topk_backward(probs, idx, dw, d_probs, ctx.renormalize,
-                                                    torch.bfloat16)
-        d_wr = None
-        if need_wr:
-            if w_router.shape[0] <= 256:
-                d_wr = ops.router_linear_backward_dw(d_logits, x)
-            else:
-                d_wr = d_logits.t().contiguous() @ x
-        d_x = None
-        if need_x:
-            d_xs = ops.gemm_gate_up_backward_dx(d_gu, plan, gate_up_proj)
-            d_x = ops.gather_backward(d_xs, plan,
-                                      addend=ops.router_linear_backward_dx(d_logits, w_router))
-        ctx.plan = None
-        return d_x, d_wr, d_w1, d_w2, None, None, None
+from .router import gating_linear, sigmoid_topk, softmax_topk
 
 
 def _fused_softmax_ok(x, w_router, gate_up_proj, down_proj) -> bool:
@@ -102,17 +36,26 @@ def moe_layer(x: torch.Tensor, w_router: torch.Tensor, gate_up_proj: torch.Tenso
         raise ValueError(f"unknown gating {gating!r}")
     hip = gating == "hip"
     if router == "softmax" and hip and _fused_softmax_ok(x, w_router, gate_up_proj, down_proj):
-        return SoftmaxMoELayerFunction.apply(x.contiguous(), w_router, gate_up_proj.contiguous(),
-                                             down_proj.contiguous(), top_k, renormalize,
-                                             logit_offset)
+        # Gating linear + softmax router + experts as ONE autograd node (op
+        # moe_amd::moe_layer_fwd), so that the two gradients of the hidden
+        # states (through the gating linear and through the experts) meet
+        # inside the gather backward (addend = the gating linear's dX)
+        # instead of in autograd's separate add.  The arithmetic is that of
+        # the composed path below: every rounding point is kept, only the
+        # fp32 summation orders of the two router GEMMs differ.
+        save = torch.is_grad_enabled() and any(
+            t.requires_grad for t in (x, w_router, gate_up_proj, down_proj))
+        res = torch.ops.moe_amd.moe_layer_fwd(x.contiguous(), w_router, gate_up_proj.contiguous(),
+                                              down_proj.contiguous(), int(top_k),
+                                              bool(renormalize), logit_offset, save)
+        return res[0], res[1], res[2], res[3]
     if router == "softmax":
         logits = gating_linear(x, w_router, fp32=False, hip=hip)
-        probs, w, idx = SoftmaxTopKFunction.apply(logits, top_k, renormalize, logit_offset)
+        probs, w, idx = softmax_topk(logits, top_k, renormalize, logit_offset)
     elif router == "sigmoid":
         logits = gating_linear(x, w_router, fp32=True, hip=hip)
-        probs, w, idx = SigmoidTopKFunction.apply(logits, expert_bias, top_k, renormalize,
-                                                  scaling_factor, num_groups, group_topk,
-                                                  x.dtype, tokens_per_expert)
+        probs, w, idx = sigmoid_topk(logits, expert_bias, top_k, renormalize, scaling_factor,
+                                     num_groups, group_topk, x.dtype, tokens_per_expert)
     else:
         raise ValueError(f"unknown router {router!r}")
     out = experts_forward(x, idx, w, gate_up_proj, down_proj)

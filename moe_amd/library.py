@@ -1,0 +1,438 @@
+"""torch.library registrations of the HIP expert layer and routers.
+
+The reference's experts backend registers its grouped GEMM as a custom op
+with a fake (shape) implementation and an autograd formula
+(transformers/integrations/moe.py:245-257), so that torch.compile traces the
+layer without a graph break.  The same contract holds here for every
+differentiable piece of the MI355X path, each a functional op in namespace
+``moe_amd``:
+
+  experts_fwd / experts_bwd      the expert layer (permute, GEMM-1 + SwiGLU,
+                                 GEMM-2, combine; fused backward)
+  moe_layer_fwd / moe_layer_bwd  gating linear + softmax router + experts as
+                                 one node (the two hidden-state gradients meet
+                                 inside the gather backward)
+  router_linear / _backward      the gating linear on the MFMA kernel
+  softmax_topk / _backward       Qwen3MoeTopKRouter's softmax + top-k
+  sigmoid_topk / _backward       DeepSeekRouter's sigmoid + biased top-k
+
+A forward op returns, besides its results, the tensors its backward needs
+(the routing plan, gate_up), so that setup_context saves only op outputs; the
+public functions in experts.py, router.py and layer.py return the results.
+Ops run their HIP entry points on torch's current stream; the fake
+implementations only compute output shapes (the tile plan's byte size is a
+host function of S and E, or an unbacked size under symbolic shapes).
+Gradients that a caller does not need come back as empty tensors from the
+backward ops and as None from autograd.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+from torch import Tensor
+
+from . import _lib, ops
+
+_LIB = "moe_amd"
+
+
+def _plan_bytes(S, E) -> int:
+    if isinstance(S, int) and isinstance(E, int):
+        return int(_lib.load().moe_amd_tile_plan_size(S, E))
+    return torch.library.get_ctx().new_dynamic_size()
+
+
+def _plan_fake(S, E, dev):
+    i32 = dict(device=dev, dtype=torch.int32)
+    return (torch.empty(E, **i32), torch.empty(E + 1, **i32), torch.empty(S, **i32),
+            torch.empty(S, **i32), torch.empty(_plan_bytes(S, E), device=dev, dtype=torch.uint8))
+
+
+def _plan(counts, offsets, row_src, slot, tile_plan, E, K, T) -> ops.RoutingPlan:
+    return ops.RoutingPlan(counts, offsets, row_src, slot, tile_plan, E, K, T)
+
+
+def _empty_like_none(t: Tensor) -> Tensor:
+    return t.new_empty(0)
+
+
+# ------------------------------------------------------------------ experts
+
+@torch.library.custom_op(f"{_LIB}::experts_fwd", mutates_args=())
+def experts_fwd(hidden_states: Tensor, top_k_index: Tensor, top_k_weights: Tensor,
+                gate_up_proj: Tensor, down_proj: Tensor, save_for_backward: bool
+                ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """(out [T,H], gate_up [S,2I] or [0,2I], counts, offsets, row_src, slot,
+    tile_plan).  transformers/integrations/moe.py:377-478."""
+    plan = ops.permute(top_k_index, gate_up_proj.shape[0])
+    gu, act = ops.gemm_gate_up_swiglu(hidden_states, plan, gate_up_proj,
+                                      save_gate_up=save_for_backward)
+    y = ops.gemm_down(act, plan, down_proj)
+    del act
+    out = ops.combine(y, plan, top_k_weights)
+    if gu is None:
+        gu = hidden_states.new_empty(0, gate_up_proj.shape[1])
+    return out, gu, plan.counts, plan.offsets, plan.row_src, plan.slot, plan.tile_plan
+
+
+@experts_fwd.register_fake
+def _(hidden_states, top_k_index, top_k_weights, gate_up_proj, down_proj, save_for_backward):
+    T, H = hidden_states.shape
+    S = T * top_k_index.shape[1]
+    E, I2 = gate_up_proj.shape[0], gate_up_proj.shape[1]
+    out = hidden_states.new_empty(T, H)
+    gu = hidden_states.new_empty(S if save_for_backward else 0, I2)
+    return (out, gu) + _plan_fake(S, E, hidden_states.device)
+
+
+@torch.library.custom_op(f"{_LIB}::experts_bwd", mutates_args=())
+def experts_bwd(d_out: Tensor, hidden_states: Tensor, top_k_weights: Tensor, gate_up_proj: Tensor,
+                down_proj: Tensor, gate_up: Tensor, counts: Tensor, offsets: Tensor,
+                row_src: Tensor, slot: Tensor, tile_plan: Tensor, need_x: bool, need_w1: bool,
+                need_w2: bool) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """(d_x, d_topk_weights, d_gate_up_proj, d_down_proj); the combine's
+    backward runs fused into GEMM-2's (formulas integrations/moe.py:226-242)."""
+    T, K = top_k_weights.shape
+    plan = _plan(counts, offsets, row_src, slot, tile_plan, gate_up_proj.shape[0], K, T)
+    d_out = d_out.to(hidden_states.dtype).contiguous()
+    d_gu, act_w, dw = ops.gemm_down_backward_fused(d_out, plan, down_proj, gate_up, top_k_weights)
+    d_w2 = (ops.gemm_down_backward_dw_gathered(d_out, act_w, plan, down_proj.shape)
+            if need_w2 else _empty_like_none(down_proj))
+    del act_w
+    d_w1 = (ops.gemm_gate_up_backward_dw(d_gu, hidden_states, plan, gate_up_proj.shape)
+            if need_w1 else _empty_like_none(gate_up_proj))
+    if need_x:
+        d_x = ops.gather_backward(ops.gemm_gate_up_backward_dx(d_gu, plan, gate_up_proj), plan)
+    else:
+        d_x = _empty_like_none(hidden_states)
+    return d_x, dw, d_w1, d_w2
+
+
+@experts_bwd.register_fake
+def _(d_out, hidden_states, top_k_weights, gate_up_proj, down_proj, gate_up, counts, offsets,
+      row_src, slot, tile_plan, need_x, need_w1, need_w2):
+    return (torch.empty_like(hidden_states) if need_x else hidden_states.new_empty(0),
+            torch.empty_like(top_k_weights),
+            torch.empty_like(gate_up_proj) if need_w1 else gate_up_proj.new_empty(0),
+            torch.empty_like(down_proj) if need_w2 else down_proj.new_empty(0))
+
+
+def _experts_setup(ctx, inputs, output):
+    x, _, w, w1, w2, _ = inputs
+    _, gu, counts, offsets, row_src, slot, tile_plan = output
+    ctx.save_for_backward(x, w, w1, w2, gu, counts, offsets, row_src, slot, tile_plan)
+
+
+def _experts_backward(ctx, d_out, *unused):
+    need_x, _, need_w, need_w1, need_w2 = ctx.needs_input_grad[:5]
+    d_x, d_w, d_w1, d_w2 = torch.ops.moe_amd.experts_bwd(
+        d_out, *ctx.saved_tensors, bool(need_x), bool(need_w1), bool(need_w2))
+    return (d_x if need_x else None, None, d_w if need_w else None, d_w1 if need_w1 else None,
+            d_w2 if need_w2 else None, None)
+
+
+torch.library.register_autograd(f"{_LIB}::experts_fwd", _experts_backward,
+                                setup_context=_experts_setup)
+
+
+# ----------------------------------------------------------- gating linear
+
+@torch.library.custom_op(f"{_LIB}::router_linear", mutates_args=())
+def router_linear(x: Tensor, weight: Tensor, out_dtype: torch.dtype) -> Tensor:
+    """logits = x . W^T, fp32 accumulation, logits in out_dtype (bf16:
+    src/models/modeling_qwen3_moe.py:268-270; fp32: src/models/router.py:107-109)."""
+    return ops.router_linear(x, weight, out_dtype)
+
+
+@router_linear.register_fake
+def _(x, weight, out_dtype):
+    return x.new_empty(x.shape[0], weight.shape[0], dtype=out_dtype)
+
+
+@torch.library.custom_op(f"{_LIB}::router_linear_backward", mutates_args=())
+def router_linear_backward(d_logits: Tensor, x: Tensor, weight: Tensor, out_dtype: torch.dtype,
+                           need_x: bool, need_w: bool) -> tuple[Tensor, Tensor]:
+    """(d_x, d_W).  bf16 logits: the MFMA dX and split-K dW kernels (fp32
+    accumulation, one bf16 rounding, as F.linear's bf16 backward) where H is a
+    multiple of 256 (dW: E <= 256), else torch in bf16; fp32 logits: torch in
+    fp32, cast to the inputs' dtypes."""
+    E, H = weight.shape
+    dx = x.new_empty(0)
+    dw = weight.new_empty(0)
+    if out_dtype == torch.float32:
+        g = d_logits.float()
+        if need_x:
+            dx = (g @ weight.float()).to(x.dtype)
+        if need_w:
+            dw = (g.t().contiguous() @ x.float()).to(weight.dtype)
+    else:
+        g = d_logits.to(x.dtype)
+        if need_x:
+            dx = ops.router_linear_backward_dx(g, weight) if H % 256 == 0 else g @ weight
+        if need_w:
+            dw = (ops.router_linear_backward_dw(g, x) if H % 256 == 0 and E <= 256
+                  else g.t().contiguous() @ x)
+    return dx, dw
+
+
+@router_linear_backward.register_fake
+def _(d_logits, x, weight, out_dtype, need_x, need_w):
+    return (torch.empty_like(x) if need_x else x.new_empty(0),
+            torch.empty_like(weight) if need_w else weight.new_empty(0))
+
+
+def _linear_setup(ctx, inputs, output):
+    x, weight, out_dtype = inputs
+    ctx.save_for_backward(x, weight)
+    ctx.out_dtype = out_dtype
+
+
+def _linear_backward(ctx, d_logits):
+    x, weight = ctx.saved_tensors
+    need_x, need_w = ctx.needs_input_grad[:2]
+    dx, dw = torch.ops.moe_amd.router_linear_backward(d_logits, x, weight, ctx.out_dtype,
+                                                      bool(need_x), bool(need_w))
+    return (dx if need_x else None, dw if need_w else None, None)
+
+
+torch.library.register_autograd(f"{_LIB}::router_linear", _linear_backward,
+                                setup_context=_linear_setup)
+
+
+# ---------------------------------------------------------- softmax router
+
+@torch.library.custom_op(f"{_LIB}::softmax_topk", mutates_args=())
+def softmax_topk(logits: Tensor, top_k: int, renormalize: bool,
+                 logit_offset: Optional[Tensor]) -> tuple[Tensor, Tensor, Tensor]:
+    """(probs fp32 [T,E], weights fp32 [T,K], index int64 [T,K]);
+    src/models/modeling_qwen3_moe.py:266-275."""
+    return ops.router_softmax_topk(logits, top_k, renormalize, logit_offset)
+
+
+@softmax_topk.register_fake
+def _(logits, top_k, renormalize, logit_offset):
+    T, E = logits.shape
+    f32 = dict(device=logits.device, dtype=torch.float32)
+    return (torch.empty(T, E, **f32), torch.empty(T, top_k, **f32),
+            torch.empty(T, top_k, device=logits.device, dtype=torch.int64))
+
+
+@torch.library.custom_op(f"{_LIB}::softmax_topk_backward", mutates_args=())
+def softmax_topk_backward(probs: Tensor, topk_index: Tensor, d_weights: Optional[Tensor],
+                          d_probs: Optional[Tensor], renormalize: bool,
+                          logits_dtype: torch.dtype) -> Tensor:
+    """d_logits [T,E] in the logits' dtype (autograd of :266-275)."""
+    if d_weights is None:
+        d_weights = torch.zeros(topk_index.shape, device=probs.device, dtype=torch.float32)
+    return ops.router_softmax_topk_backward(probs, topk_index, d_weights, d_probs, renormalize,
+                                            logits_dtype)
+
+
+@softmax_topk_backward.register_fake
+def _(probs, topk_index, d_weights, d_probs, renormalize, logits_dtype):
+    return torch.empty_like(probs, dtype=logits_dtype)
+
+
+def _softmax_setup(ctx, inputs, output):
+    logits, _, renormalize, _ = inputs
+    probs, _, idx = output
+    ctx.set_materialize_grads(False)
+    ctx.mark_non_differentiable(idx)
+    ctx.save_for_backward(probs, idx)
+    ctx.renormalize = renormalize
+    ctx.logits_dtype = logits.dtype
+
+
+def _softmax_backward(ctx, d_probs, d_w, d_idx):
+    probs, idx = ctx.saved_tensors
+    if d_probs is None and d_w is None:
+        return None, None, None, None
+    d_logits = torch.ops.moe_amd.softmax_topk_backward(probs, idx, d_w, d_probs, ctx.renormalize,
+                                                       ctx.logits_dtype)
+    return d_logits, None, None, None
+
+
+torch.library.register_autograd(f"{_LIB}::softmax_topk", _softmax_backward,
+                                setup_context=_softmax_setup)
+
+
+# --------------------------------------------------------- DeepSeek router
+
+@torch.library.custom_op(f"{_LIB}::sigmoid_topk", mutates_args=())
+def sigmoid_topk(logits: Tensor, expert_bias: Optional[Tensor], top_k: int, renormalize: bool,
+                 scaling_factor: float, num_groups: int, group_topk: int,
+                 weights_dtype: torch.dtype, count: bool
+                 ) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """(scores fp32 [T,E], weights [T,K] in weights_dtype, index int64 [T,K],
+    selection counts fp32 [E] (zeros unless count)); src/models/router.py:
+    103-155.  scaling_factor 0 = none; num_groups/group_topk 0 = flat top-k.
+    The counts come back as an output (the op is functional); the router adds
+    them to its local_tokens_per_expert buffer."""
+    counts = torch.zeros(logits.shape[1], device=logits.device, dtype=torch.float32)
+    scores, w, idx = ops.router_sigmoid_topk(
+        logits, expert_bias, top_k, renormalize, scaling_factor or None,
+        num_groups or None, group_topk or None, weights_dtype, counts if count else None)
+    return scores, w, idx, counts
+
+
+@sigmoid_topk.register_fake
+def _(logits, expert_bias, top_k, renormalize, scaling_factor, num_groups, group_topk,
+      weights_dtype, count):
+    T, E = logits.shape
+    dev = logits.device
+    return (torch.empty(T, E, device=dev, dtype=torch.float32),
+            torch.empty(T, top_k, device=dev, dtype=weights_dtype),
+            torch.empty(T, top_k, device=dev, dtype=torch.int64),
+            torch.empty(E, device=dev, dtype=torch.float32))
+
+
+@torch.library.custom_op(f"{_LIB}::sigmoid_topk_backward", mutates_args=())
+def sigmoid_topk_backward(scores: Tensor, topk_index: Tensor, d_weights: Tensor,
+                          d_scores: Optional[Tensor], renormalize: bool,
+                          scaling_factor: float) -> Tensor:
+    """d_logits [T,E] fp32 (autograd of router.py:112-140)."""
+    return ops.router_sigmoid_topk_backward(scores, topk_index, d_weights, d_scores, renormalize,
+                                            scaling_factor or None)
+
+
+@sigmoid_topk_backward.register_fake
+def _(scores, topk_index, d_weights, d_scores, renormalize, scaling_factor):
+    return torch.empty_like(scores)
+
+
+def _sigmoid_setup(ctx, inputs, output):
+    _, _, _, renormalize, scaling_factor, _, _, weights_dtype, _ = inputs
+    scores, _, idx, counts = output
+    ctx.set_materialize_grads(False)
+    ctx.mark_non_differentiable(idx, counts)
+    ctx.save_for_backward(scores, idx)
+    ctx.renormalize = renormalize
+    ctx.scaling_factor = scaling_factor
+    ctx.w_dtype = weights_dtype
+
+
+def _sigmoid_backward(ctx, d_scores, d_w, d_idx, d_counts):
+    scores, idx = ctx.saved_tensors
+    none = (None,) * 8
+    if d_scores is None and d_w is None:
+        return (None,) + none
+    if d_w is None:
+        d_w = torch.zeros(idx.shape, device=idx.device, dtype=ctx.w_dtype)
+    d_logits = torch.ops.moe_amd.sigmoid_topk_backward(scores, idx, d_w.to(ctx.w_dtype), d_scores,
+                                                       ctx.renormalize, ctx.scaling_factor)
+    return (d_logits,) + none
+
+
+torch.library.register_autograd(f"{_LIB}::sigmoid_topk", _sigmoid_backward,
+                                setup_context=_sigmoid_setup)
+
+
+# ------------------------------------------------ softmax layer, one node
+
+@torch.library.custom_op(f"{_LIB}::moe_layer_fwd", mutates_args=())
+def moe_layer_fwd(x: Tensor, w_router: Tensor, gate_up_proj: Tensor, down_proj: Tensor,
+                  top_k: int, renormalize: bool, logit_offset: Optional[Tensor],
+                  save_for_backward: bool
+                  ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor,
+                             Tensor, Tensor]:
+    """(out, probs fp32, weights fp32, index, gate_up, counts, offsets, row_src,
+    slot, tile_plan): bf16 gating linear (MFMA), softmax router, experts
+    (Qwen3MoeSparseMoeBlock.forward, src/models/modeling_qwen3_moe.py:284-289)."""
+    logits = ops.router_linear(x, w_router, torch.bfloat16)
+    probs, w, idx = ops.router_softmax_topk(logits, top_k, renormalize, logit_offset)
+    del logits
+    plan = ops.permute(idx, gate_up_proj.shape[0])
+    gu, act = ops.gemm_gate_up_swiglu(x, plan, gate_up_proj, save_gate_up=save_for_backward)
+    y = ops.gemm_down(act, plan, down_proj)
+    del act
+    out = ops.combine(y, plan, w)
+    if gu is None:
+        gu = x.new_empty(0, gate_up_proj.shape[1])
+    return (out, probs, w, idx, gu, plan.counts, plan.offsets, plan.row_src, plan.slot,
+            plan.tile_plan)
+
+
+@moe_layer_fwd.register_fake
+def _(x, w_router, gate_up_proj, down_proj, top_k, renormalize, logit_offset, save_for_backward):
+    T, H = x.shape
+    E, I2 = gate_up_proj.shape[0], gate_up_proj.shape[1]
+    S = T * top_k
+    dev = x.device
+    f32 = dict(device=dev, dtype=torch.float32)
+    return (x.new_empty(T, H), torch.empty(T, E, **f32), torch.empty(T, top_k, **f32),
+            torch.empty(T, top_k, device=dev, dtype=torch.int64),
+            x.new_empty(S if save_for_backward else 0, I2)) + _plan_fake(S, E, dev)
+
+
+@torch.library.custom_op(f"{_LIB}::moe_layer_bwd", mutates_args=())
+def moe_layer_bwd(d_out: Optional[Tensor], d_probs: Optional[Tensor], d_w: Optional[Tensor],
+                  x: Tensor, w_router: Tensor, gate_up_proj: Tensor, down_proj: Tensor,
+                  gate_up: Tensor, probs: Tensor, w: Tensor, idx: Tensor, counts: Tensor,
+                  offsets: Tensor, row_src: Tensor, slot: Tensor, tile_plan: Tensor,
+                  renormalize: bool, need_x: bool, need_wr: bool, need_w1: bool, need_w2: bool
+                  ) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """(d_x, d_w_router, d_gate_up_proj, d_down_proj).  The combine backward
+    runs fused into GEMM-2's; the gating linear's dX is added inside the
+    gather backward."""
+    T, K = idx.shape
+    plan = _plan(counts, offsets, row_src, slot, tile_plan, gate_up_proj.shape[0], K, T)
+    if d_out is None:
+        d_out = torch.zeros(x.shape, dtype=x.dtype, device=x.device)
+    d_out = d_out.to(x.dtype).contiguous()
+    d_gu, act_w, dw = ops.gemm_down_backward_fused(d_out, plan, down_proj, gate_up, w)
+    d_w2 = (ops.gemm_down_backward_dw_gathered(d_out, act_w, plan, down_proj.shape)
+            if need_w2 else down_proj.new_empty(0))
+    del act_w
+    d_w1 = (ops.gemm_gate_up_backward_dw(d_gu, x, plan, gate_up_proj.shape)
+            if need_w1 else gate_up_proj.new_empty(0))
+    if d_w is not None:
+        dw = dw + d_w.float()
+    d_logits = ops.router_softmax_topk_backward(probs, idx, dw, d_probs, renormalize,
+                                                torch.bfloat16)
+    d_wr = w_router.new_empty(0)
+    if need_wr:
+        if w_router.shape[0] <= 256:
+            d_wr = ops.router_linear_backward_dw(d_logits, x)
+        else:
+            d_wr = d_logits.t().contiguous() @ x
+    d_x = x.new_empty(0)
+    if need_x:
+        d_xs = ops.gemm_gate_up_backward_dx(d_gu, plan, gate_up_proj)
+        d_x = ops.gather_backward(d_xs, plan,
+                                  addend=ops.router_linear_backward_dx(d_logits, w_router))
+    return d_x, d_wr, d_w1, d_w2
+
+
+@moe_layer_bwd.register_fake
+def _(d_out, d_probs, d_w, x, w_router, gate_up_proj, down_proj, gate_up, probs, w, idx, counts,
+      offsets, row_src, slot, tile_plan, renormalize, need_x, need_wr, need_w1, need_w2):
+    return (torch.empty_like(x) if need_x else x.new_empty(0),
+            torch.empty_like(w_router) if need_wr else w_router.new_empty(0),
+            torch.empty_like(gate_up_proj) if need_w1 else gate_up_proj.new_empty(0),
+            torch.empty_like(down_proj) if need_w2 else down_proj.new_empty(0))
+
+
+def _layer_setup(ctx, inputs, output):
+    x, w_router, gate_up_proj, down_proj, _, renormalize, _, _ = inputs
+    _, probs, w, idx, gu, counts, offsets, row_src, slot, tile_plan = output
+    ctx.set_materialize_grads(False)
+    ctx.mark_non_differentiable(idx)
+    ctx.save_for_backward(x, w_router, gate_up_proj, down_proj, gu, probs, w, idx, counts,
+                          offsets, row_src, slot, tile_plan)
+    ctx.renormalize = renormalize
+
+
+def _layer_backward(ctx, d_out, d_probs, d_w, *unused):
+    need_x, need_wr, need_w1, need_w2 = (bool(n) for n in ctx.needs_input_grad[:4])
+    if d_out is None and d_probs is None and d_w is None:
+        return (None,) * 8
+    d_x, d_wr, d_w1, d_w2 = torch.ops.moe_amd.moe_layer_bwd(
+        d_out, d_probs, d_w, *ctx.saved_tensors, ctx.renormalize, need_x, need_wr, need_w1,
+        need_w2)
+    return (d_x if need_x else None, d_wr if need_wr else None, d_w1 if need_w1 else None,
+            d_w2 if need_w2 else None, None, None, None, None)
+
+
+torch.library.register_autograd(f"{_LIB}::moe_layer_fwd", _layer_backward,
+                                setup_context=_layer_setup)

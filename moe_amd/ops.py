@@ -251,7 +251,9 @@ def permute(topk_index: torch.Tensor, num_experts: int) -> RoutingPlan:
     row_src = torch.empty(S, device=dev, dtype=torch.int32)
     slot = torch.empty(S, device=dev, dtype=torch.int32)
     plan_bytes = int(lib.moe_amd_tile_plan_size(S, E))
-    tile_plan = torch.empty(plan_bytes, device=dev, dtype=torch.uint8)
+    # zeroed so that the bytes the permutation leaves unwritten (alignment
+    # padding, tile-table entries past the tile count) are deterministic too
+    tile_plan = torch.zeros(plan_bytes, device=dev, dtype=torch.uint8)
     _call("moe_amd_permute", topk_index.data_ptr(), S, E, ws.data_ptr(), ws.numel(),
           counts.data_ptr(), offsets.data_ptr(), row_src.data_ptr(), slot.data_ptr(),
           tile_plan.data_ptr(), plan_bytes, _stream(topk_index))

@@ -17,7 +17,7 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
-from . import ops
+from . import library  # noqa: F401  (registers the moe_amd:: ops)
 
 try:  # the plug-in base class of the reference's routers
     from transformers.models.qwen3_moe.modeling_qwen3_moe import Qwen3MoeTopKRouter as _RouterBase
@@ -32,40 +32,12 @@ except Exception:  # pragma: no cover - transformers absent: plain module base
             self.weight = nn.Parameter(torch.zeros(self.num_experts, self.hidden_dim))
 
 
-class RouterLinearFunction(torch.autograd.Function):
+def router_linear(x: torch.Tensor, weight: torch.Tensor, out_dtype: torch.dtype) -> torch.Tensor:
     """logits = x . W^T on the MFMA kernel (bf16 inputs, fp32 accumulation),
     logits in bf16 (F.linear on bf16 tensors, src/models/modeling_qwen3_moe.py:
     268-270) or fp32 (F.linear(h.float(), W.float()), src/models/router.py:
-    107-109).  The backward for bf16 logits runs on the MFMA dX and split-K dW
-    kernels (fp32 accumulation, one bf16 rounding, as F.linear's bf16
-    backward) where H is a multiple of 256 (dW: E <= 256), else torch in bf16;
-    for fp32 logits it is torch in fp32, cast to the inputs' dtypes."""
-
-    @staticmethod
-    def forward(ctx, x, weight, out_dtype):
-        ctx.save_for_backward(x, weight)
-        ctx.out_dtype = out_dtype
-        return ops.router_linear(x, weight, out_dtype)
-
-    @staticmethod
-    def backward(ctx, d_logits):
-        x, weight = ctx.saved_tensors
-        dx = dw = None
-        if ctx.out_dtype == torch.float32:
-            g = d_logits.float()
-            if ctx.needs_input_grad[0]:
-                dx = (g @ weight.float()).to(x.dtype)
-            if ctx.needs_input_grad[1]:
-                dw = (g.t().contiguous() @ x.float()).to(weight.dtype)
-        else:
-            g = d_logits.to(x.dtype)
-            E, H = weight.shape
-            if ctx.needs_input_grad[0]:
-                dx = ops.router_linear_backward_dx(g, weight) if H % 256 == 0 else g @ weight
-            if ctx.needs_input_grad[1]:
-                dw = (ops.router_linear_backward_dw(g, x) if H % 256 == 0 and E <= 256
-                      else g.t().contiguous() @ x)
-        return dx, dw, None
+    107-109); differentiable (op ``moe_amd::router_linear``)."""
+    return torch.ops.moe_amd.router_linear(x, weight, out_dtype)
 
 
 def gating_linear(x: torch.Tensor, weight: torch.Tensor, fp32: bool, hip: bool = True):
@@ -76,58 +48,35 @@ def gating_linear(x: torch.Tensor, weight: torch.Tensor, fp32: bool, hip: bool =
     E, H = weight.shape
     if (hip and x.is_cuda and x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16
             and H % 64 == 0 and E % 8 == 0):
-        return RouterLinearFunction.apply(x, weight, torch.float32 if fp32 else torch.bfloat16)
+        return router_linear(x, weight, torch.float32 if fp32 else torch.bfloat16)
     if fp32:
         return F.linear(x.float(), weight.float())
     return F.linear(x, weight)
 
 
-class SoftmaxTopKFunction(torch.autograd.Function):
-    """(logits) -> (probs, weights, index) with the softmax router's backward."""
-
-    @staticmethod
-    def forward(ctx, logits, top_k, renormalize, logit_offset):
-        probs, w, idx = ops.router_softmax_topk(logits, top_k, renormalize, logit_offset)
-        ctx.save_for_backward(probs, idx)
-        ctx.renormalize = renormalize
-        ctx.logits_dtype = logits.dtype
-        ctx.mark_non_differentiable(idx)
-        return probs, w, idx
-
-    @staticmethod
-    def backward(ctx, d_probs, d_w, d_idx):
-        probs, idx = ctx.saved_tensors
-        if d_w is None:
-            d_w = torch.zeros(idx.shape, device=idx.device, dtype=torch.float32)
-        d_logits = ops.router_softmax_topk_backward(probs, idx, d_w, d_probs, ctx.renormalize,
-                                                    ctx.logits_dtype)
-        return d_logits, None, None, None
+def softmax_topk(logits: torch.Tensor, top_k: int, renormalize: bool = True,
+                 logit_offset: torch.Tensor | None = None):
+    """(logits) -> (probs fp32 [T,E], weights fp32 [T,K], index [T,K]) with
+    the softmax router's backward (op ``moe_amd::softmax_topk``)."""
+    return torch.ops.moe_amd.softmax_topk(logits, int(top_k), bool(renormalize), logit_offset)
 
 
-class SigmoidTopKFunction(torch.autograd.Function):
-    """(fp32 logits) -> (scores, weights, index) for the DeepSeek-V3 router."""
-
-    @staticmethod
-    def forward(ctx, logits, expert_bias, top_k, renormalize, scaling_factor, num_groups,
-                group_topk, weights_dtype, tokens_per_expert):
-        scores, w, idx = ops.router_sigmoid_topk(
-            logits, expert_bias, top_k, renormalize, scaling_factor, num_groups, group_topk,
-            weights_dtype, tokens_per_expert)
-        ctx.save_for_backward(scores, idx)
-        ctx.renormalize = renormalize
-        ctx.scaling_factor = scaling_factor
-        ctx.w_dtype = weights_dtype
-        ctx.mark_non_differentiable(idx)
-        return scores, w, idx
-
-    @staticmethod
-    def backward(ctx, d_scores, d_w, d_idx):
-        scores, idx = ctx.saved_tensors
-        if d_w is None:
-            d_w = torch.zeros(idx.shape, device=idx.device, dtype=ctx.w_dtype)
-        d_logits = ops.router_sigmoid_topk_backward(scores, idx, d_w.to(ctx.w_dtype), d_scores,
-                                                    ctx.renormalize, ctx.scaling_factor)
-        return d_logits, None, None, None, None, None, None, None, None
+def sigmoid_topk(logits: torch.Tensor, expert_bias: torch.Tensor | None, top_k: int,
+                 renormalize: bool = True, scaling_factor: float | None = None,
+                 num_groups: int | None = None, group_topk: int | None = None,
+                 weights_dtype: torch.dtype = torch.float32,
+                 tokens_per_expert: torch.Tensor | None = None):
+    """(fp32 logits) -> (scores, weights, index) for the DeepSeek-V3 router
+    (op ``moe_amd::sigmoid_topk``); with ``tokens_per_expert`` the selection
+    counts of this call are added to it (src/models/router.py:143-150)."""
+    grouped = num_groups is not None and group_topk is not None
+    scores, w, idx, counts = torch.ops.moe_amd.sigmoid_topk(
+        logits, expert_bias, int(top_k), bool(renormalize), float(scaling_factor or 0.0),
+        int(num_groups) if grouped else 0, int(group_topk) if grouped else 0, weights_dtype,
+        tokens_per_expert is not None)
+    if tokens_per_expert is not None:
+        tokens_per_expert.add_(counts)
+    return scores, w, idx
 
 
 class MI355XTopKRouter(_RouterBase):
@@ -147,8 +96,7 @@ class MI355XTopKRouter(_RouterBase):
     def forward(self, hidden_states):
         hidden_states = hidden_states.reshape(-1, self.hidden_dim)
         logits = gating_linear(hidden_states, self.weight, fp32=False, hip=self.hip_gating_linear)
-        return SoftmaxTopKFunction.apply(logits, self.top_k, bool(self.norm_topk_prob),
-                                         self.logit_offset)
+        return softmax_topk(logits, self.top_k, bool(self.norm_topk_prob), self.logit_offset)
 
     @classmethod
     def from_router(cls, old: nn.Module) -> "MI355XTopKRouter":
@@ -184,7 +132,7 @@ class MI355XDeepSeekRouter(_RouterBase):
         hidden_states = hidden_states.reshape(-1, self.hidden_dim)
         logits = gating_linear(hidden_states, self.weight, fp32=True, hip=self.hip_gating_linear)
         counting = torch.is_grad_enabled()
-        scores, w, idx = SigmoidTopKFunction.apply(
+        scores, w, idx = sigmoid_topk(
             logits, self.expert_bias, self.top_k, bool(self.norm_topk_prob), self.scaling_factor,
             self.num_groups, self.group_topk, hidden_states.dtype,
             self.local_tokens_per_expert if counting else None)

@@ -147,12 +147,12 @@ def test_l_shape_sampled_parity():
     """L (Qwen3-30B-A3B) shape end to end on the full T=65536 batch: routing
     bit-exact for every token; outputs, dX and d(weights) on a 256-token
     sample; dW of the most- and least-loaded experts from all their tokens."""
-    from moe_amd.router import SoftmaxTopKFunction
+    from moe_amd.router import softmax_topk
     cfg = CONFIGS["l"]
     print("L shape sampled parity", flush=True)
     inp = make_inputs(cfg, seed=0, device=DEV)
     logits = F.linear(inp.x, inp.w_router)
-    _, w, idx = SoftmaxTopKFunction.apply(logits, cfg.K, True, None)
+    _, w, idx = softmax_topk(logits, cfg.K, True, None)
     xe = inp.x.clone().requires_grad_(True)
     wl = w.detach().clone().requires_grad_(True)
     w1 = inp.gate_up_proj.clone().requires_grad_(True)
@@ -229,14 +229,13 @@ def test_hip_gating_linear_matches_torch_gating():
 
 
 def test_fused_softmax_layer_matches_composed_nodes():
-    """The one-node softmax layer (SoftmaxMoELayerFunction, chosen by moe_layer
-    for bf16 inputs) against the same arithmetic as three autograd nodes
-    (RouterLinearFunction -> SoftmaxTopKFunction -> MoEExpertsFunction): the
-    forward, the expert-weight and router-weight gradients are bit-identical;
-    d_x differs only through the gating linear's dX summation order (MFMA
-    kernel vs torch), i.e. within one bf16 rounding of the router term."""
-    from moe_amd.layer import SoftmaxMoELayerFunction
-    from moe_amd.router import RouterLinearFunction, SoftmaxTopKFunction
+    """The one-node softmax layer (op moe_amd::moe_layer_fwd, chosen by
+    moe_layer for bf16 inputs) against the same arithmetic as three autograd
+    nodes (router_linear -> softmax_topk -> experts_fwd): the forward, the
+    expert-weight and router-weight gradients are bit-identical; d_x differs
+    only through the gating linear's dX summation order (MFMA kernel vs
+    torch), i.e. within one bf16 rounding of the router term."""
+    from moe_amd.router import router_linear, softmax_topk
     cfg = CONFIGS["l"].scaled(4096)
     inp = make_inputs(cfg, seed=1, device=DEV)
     outs = []
@@ -246,10 +245,10 @@ def test_fused_softmax_layer_matches_composed_nodes():
         w1 = inp.gate_up_proj.clone().requires_grad_(True)
         w2 = inp.down_proj.clone().requires_grad_(True)
         if fused:
-            out, probs, w, idx = SoftmaxMoELayerFunction.apply(x, wr, w1, w2, cfg.K, True, None)
+            out, probs, w, idx = moe_layer(x, wr, w1, w2, cfg.K)
         else:
-            logits = RouterLinearFunction.apply(x, wr, torch.bfloat16)
-            probs, w, idx = SoftmaxTopKFunction.apply(logits, cfg.K, True, None)
+            logits = router_linear(x, wr, torch.bfloat16)
+            probs, w, idx = softmax_topk(logits, cfg.K, True, None)
             out = experts_forward(x, idx, w, w1, w2)
         out.backward(inp.dout)
         outs.append((out.detach(), probs, idx, x.grad, wr.grad, w1.grad, w2.grad))

@@ -11,7 +11,7 @@ import torch
 import torch.nn.functional as F
 
 from moe_amd import ops
-from moe_amd.router import SigmoidTopKFunction, SoftmaxTopKFunction
+from moe_amd.router import sigmoid_topk, softmax_topk
 from oracle import moe_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -133,7 +133,7 @@ def test_softmax_router_backward_parity(renorm):
     g = torch.Generator().manual_seed(21)
     T, E, K = 2048, 128, 8
     logits = (torch.randn(T, E, generator=g)).to(torch.bfloat16).to(DEV).requires_grad_(True)
-    probs, w, idx = SoftmaxTopKFunction.apply(logits, K, renorm, None)
+    probs, w, idx = softmax_topk(logits, K, renorm, None)
     dw = torch.randn(T, K, generator=g).to(DEV)
     dp = torch.randn(T, E, generator=g).to(DEV) * 0.1
     (gl,) = torch.autograd.grad((w * dw).sum() + (probs * dp).sum(), logits)
@@ -148,8 +148,7 @@ def test_sigmoid_router_backward_parity():
     T, E, K = 1024, 256, 8
     logits = torch.randn(T, E, generator=g).to(DEV).requires_grad_(True)
     bias = (torch.rand(E, generator=g) - 0.5).to(DEV)
-    scores, w, idx = SigmoidTopKFunction.apply(logits, bias, K, True, 2.5, None, None,
-                                               torch.float32, None)
+    scores, w, idx = sigmoid_topk(logits, bias, K, True, 2.5, None, None, torch.float32, None)
     dw = torch.randn(T, K, generator=g).to(DEV)
     ds = torch.randn(T, E, generator=g).to(DEV) * 0.1
     (gl,) = torch.autograd.grad((w * dw).sum() + (scores * ds).sum(), logits)
