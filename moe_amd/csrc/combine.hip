@@ -10,12 +10,21 @@ namespace moe {
 namespace {
 
 constexpr int kWaves = 4;
+constexpr int kChunks = 1;  // 64*N-element row chunks whose loads are issued together
 
 template <typename T> struct Vec;
+// Loads and stores are non-temporal: every routed row is read once and every
+// output row written once, so they bypass the caches' retention (measured:
+// a streaming read reaches 7.0 TB/s this way against 6.3 TB/s with plain
+// loads).  load_raw keeps the 16 bytes packed (4 VGPRs) until they are
+// consumed, so more rows can be in flight per lane.
 template <> struct Vec<bf16> {
   static constexpr int N = 8;  // elements per 16-byte lane access
+  typedef u32x4 Raw;
+  __device__ static Raw load_raw(const bf16* p) { return __builtin_nontemporal_load((const u32x4*)p); }
+  __device__ static float get(const Raw& r, int i) { return (i & 1) ? bf_hi(r[i >> 1]) : bf_lo(r[i >> 1]); }
   __device__ static void load(const bf16* p, float (&v)[8]) {
-    u32x4 w = *(const u32x4*)p;
+    u32x4 w = __builtin_nontemporal_load((const u32x4*)p);
 #pragma unroll
     for (int i = 0; i < 4; ++i) { v[2 * i] = bf_lo(w[i]); v[2 * i + 1] = bf_hi(w[i]); }
   }
@@ -23,20 +32,23 @@ template <> struct Vec<bf16> {
     u32x4 w;
 #pragma unroll
     for (int i = 0; i < 4; ++i) w[i] = pack_bf2(v[2 * i], v[2 * i + 1]);
-    *(u32x4*)p = w;
+    __builtin_nontemporal_store(w, (u32x4*)p);
   }
   __device__ static float round(float v) { return round_bf(v); }
 };
 template <> struct Vec<float> {
   static constexpr int N = 4;
+  typedef f32x4 Raw;
+  __device__ static Raw load_raw(const float* p) { return __builtin_nontemporal_load((const f32x4*)p); }
+  __device__ static float get(const Raw& r, int i) { return r[i]; }
   __device__ static void load(const float* p, float (&v)[4]) {
-    f32x4 w = *(const f32x4*)p;
+    f32x4 w = __builtin_nontemporal_load((const f32x4*)p);
 #pragma unroll
     for (int i = 0; i < 4; ++i) v[i] = w[i];
   }
   __device__ static void store(float* p, const float (&v)[4]) {
     f32x4 w = {v[0], v[1], v[2], v[3]};
-    *(f32x4*)p = w;
+    __builtin_nontemporal_store(w, (f32x4*)p);
   }
   __device__ static float round(float v) { return v; }
 };
@@ -76,25 +88,33 @@ __global__ __launch_bounds__(64 * kWaves) void combine_kernel(
       int sk[KM];
       float wk[KM];
       token_rows<KM>(slot, w, wdt, t, lane, sk, wk);
-      for (int h0 = lane * N; h0 < H; h0 += 64 * N) {
-        float v[KM][N];
+      const bool rp = wdt == MOE_DTYPE_BF16 && sizeof(T) == 2;
+      for (int h0 = lane * N; h0 < H; h0 += 64 * N * kChunks) {
+        typename Vec<T>::Raw v[kChunks][KM];
 #pragma unroll
-        for (int k = 0; k < KM; ++k)
-          if (sk[k] < nvalid) Vec<T>::load(y + (int64_t)sk[k] * H + h0, v[k]);
-        float acc[N];
+        for (int c = 0; c < kChunks; ++c)
 #pragma unroll
-        for (int i = 0; i < N; ++i) acc[i] = 0.f;
+          for (int k = 0; k < KM; ++k)
+            if (sk[k] < nvalid && h0 + c * 64 * N < H)
+              v[c][k] = Vec<T>::load_raw(y + (int64_t)sk[k] * H + h0 + c * 64 * N);
 #pragma unroll
-        for (int k = 0; k < KM; ++k) {
-          if (sk[k] >= nvalid) continue;  // sentinel: masked to zero in the reference
+        for (int c = 0; c < kChunks; ++c) {
+          if (h0 + c * 64 * N >= H) break;
+          float acc[N];
 #pragma unroll
-          for (int i = 0; i < N; ++i) {
-            float prod = v[k][i] * wk[k];
-            if (wdt == MOE_DTYPE_BF16 && sizeof(T) == 2) prod = round_bf(prod);
-            acc[i] += prod;
+          for (int i = 0; i < N; ++i) acc[i] = 0.f;
+#pragma unroll
+          for (int k = 0; k < KM; ++k) {
+            if (sk[k] >= nvalid) continue;  // sentinel: masked to zero in the reference
+#pragma unroll
+            for (int i = 0; i < N; ++i) {
+              float prod = Vec<T>::get(v[c][k], i) * wk[k];
+              if (rp) prod = round_bf(prod);
+              acc[i] += prod;
+            }
           }
+          Vec<T>::store(out + t * H + h0 + c * 64 * N, acc);
         }
-        Vec<T>::store(out + t * H + h0, acc);
       }
     } else {
       for (int h0 = lane * N; h0 < H; h0 += 64 * N) {
@@ -212,22 +232,45 @@ __global__ __launch_bounds__(64 * kWaves) void gather_bwd_kernel(
     int sk[KM > 0 ? KM : 1];
     float wk[KM > 0 ? KM : 1];
     if constexpr (KM > 0) token_rows<KM>(slot, nullptr, 0, t, lane, sk, wk);
+    if constexpr (KM > 0) {
+      for (int h0 = lane * N; h0 < H; h0 += 64 * N * kChunks) {
+        typename Vec<T>::Raw v[kChunks][KM], a[kChunks];
+#pragma unroll
+        for (int c = 0; c < kChunks; ++c) {
+          if (h0 + c * 64 * N >= H) break;
+#pragma unroll
+          for (int k = 0; k < KM; ++k)
+            if (sk[k] < nvalid) v[c][k] = Vec<T>::load_raw(dxs + (int64_t)sk[k] * H + h0 + c * 64 * N);
+          if (addend) a[c] = Vec<T>::load_raw(addend + t * H + h0 + c * 64 * N);
+        }
+#pragma unroll
+        for (int c = 0; c < kChunks; ++c) {
+          if (h0 + c * 64 * N >= H) break;
+          float acc[N];
+#pragma unroll
+          for (int i = 0; i < N; ++i) acc[i] = 0.f;
+#pragma unroll
+          for (int k = 0; k < KM; ++k) {
+            if (sk[k] >= nvalid) continue;
+#pragma unroll
+            for (int i = 0; i < N; ++i) acc[i] += Vec<T>::get(v[c][k], i);
+          }
+          if (addend) {
+            // a second gradient of the same tensor: round the sum to T first,
+            // as autograd's accumulation of two T-typed gradients does
+#pragma unroll
+            for (int i = 0; i < N; ++i) acc[i] = Vec<T>::round(acc[i]) + Vec<T>::get(a[c], i);
+          }
+          Vec<T>::store(dx + t * H + h0 + c * 64 * N, acc);
+        }
+      }
+      continue;
+    }
     for (int h0 = lane * N; h0 < H; h0 += 64 * N) {
       float acc[N];
 #pragma unroll
       for (int i = 0; i < N; ++i) acc[i] = 0.f;
-      if constexpr (KM > 0) {
-        float v[KM][N];
-#pragma unroll
-        for (int k = 0; k < KM; ++k)
-          if (sk[k] < nvalid) Vec<T>::load(dxs + (int64_t)sk[k] * H + h0, v[k]);
-#pragma unroll
-        for (int k = 0; k < KM; ++k) {
-          if (sk[k] >= nvalid) continue;
-#pragma unroll
-          for (int i = 0; i < N; ++i) acc[i] += v[k][i];
-        }
-      } else {
+      {
         for (int k = 0; k < K; ++k) {
           const int s = slot[t * K + k];
           if (s >= nvalid) continue;
@@ -252,7 +295,7 @@ __global__ __launch_bounds__(64 * kWaves) void gather_bwd_kernel(
 
 int grid_tokens(int64_t ntok) {
   int64_t b = (ntok + kWaves - 1) / kWaves;
-  if (b > 8192) b = 8192;
+  if (b > 32768) b = 32768;
   return (int)(b < 1 ? 1 : b);
 }
 
