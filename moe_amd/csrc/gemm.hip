@@ -48,7 +48,11 @@
 //
 // Epilogue: accumulators are rounded to bf16 into an LDS staging tile, then
 // written out row by row with 16-byte lanes (full-line stores), applying the
-// mode's elementwise tail (SwiGLU, dSwiGLU) on the way out.
+// mode's elementwise tail (SwiGLU, dSwiGLU) on the way out.  The stores (and
+// the dX epilogue's gate_up reads) are non-temporal: each output is written
+// once and consumed by a later kernel, so it should not displace the operand
+// lines that concurrently running tiles share in L2 (measured: 1.8% less
+// time over the six GEMMs at L, G2F 4%).
 //
 // Reference: transformers/integrations/moe.py:439-459 (forward grouped_mm),
 // :226-242 (per-expert dX / dW formulas of the backward).
@@ -789,10 +793,10 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
             av[w] = pack_bf2(round_bf(g0 * fast_sigmoid(g0)) * u0, round_bf(g1 * fast_sigmoid(g1)) * u1);
           }
           if (r < cur.row_end && fok) {
-            *(u32x4*)(p.out + (int64_t)r * I + f) = av;
+            __builtin_nontemporal_store(av, (u32x4*)(p.out + (int64_t)r * I + f));
             if (p.out2) {
-              *(u32x4*)(p.out2 + (int64_t)r * I2 + f) = gv[q];
-              *(u32x4*)(p.out2 + (int64_t)r * I2 + I + f) = uv[q];
+              __builtin_nontemporal_store(gv[q], (u32x4*)(p.out2 + (int64_t)r * I2 + f));
+              __builtin_nontemporal_store(uv[q], (u32x4*)(p.out2 + (int64_t)r * I2 + I + f));
             }
           }
         }
@@ -820,8 +824,8 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
 #pragma unroll
         for (int q = 0; q < RB; ++q) {
           const int r = min(cur.row0 + (tid >> 5) + (b * RB + q) * (NTHR / 32), cur.row_end - 1);
-          g[q] = *(const u32x4*)(gsrc + (int64_t)r * I2);
-          u[q] = *(const u32x4*)(gsrc + (int64_t)r * I2 + I);
+          g[q] = __builtin_nontemporal_load((const u32x4*)(gsrc + (int64_t)r * I2));
+          u[q] = __builtin_nontemporal_load((const u32x4*)(gsrc + (int64_t)r * I2 + I));
         }
       };
       load_batch(0, gv[0], uv[0]);
@@ -867,9 +871,9 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
               p.dw_part[(int64_t)erow_s[row] * p.n_ct + cur.ct] = tot;
           }
           if (r < cur.row_end && fok) {
-            *(u32x4*)(p.out + (int64_t)r * I2 + f) = dgv;
-            *(u32x4*)(p.out + (int64_t)r * I2 + I + f) = duv;
-            if constexpr (FUSED) *(u32x4*)(p.out2 + (int64_t)r * I + f) = awv;
+            __builtin_nontemporal_store(dgv, (u32x4*)(p.out + (int64_t)r * I2 + f));
+            __builtin_nontemporal_store(duv, (u32x4*)(p.out + (int64_t)r * I2 + I + f));
+            if constexpr (FUSED) __builtin_nontemporal_store(awv, (u32x4*)(p.out2 + (int64_t)r * I + f));
           }
         }
       }
@@ -912,7 +916,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
         for (int q = 0; q < RB; ++q) {
           const int row = (tid >> 5) + (b * RB + q) * (NTHR / 32);
           const int r = (SWAP ? cur.ct * BC : cur.row0) + row;
-          if (r < nrows && fok) *(u32x4*)(obase + (int64_t)r * ld + f) = v[q];
+          if (r < nrows && fok) __builtin_nontemporal_store(v[q], (u32x4*)(obase + (int64_t)r * ld + f));
         }
       }
     }
