@@ -356,7 +356,7 @@ extern "C" int moe_amd_combine(const void* y, const int32_t* slot, const int32_t
   if (rc) return rc;
   MOE_REQUIRE(weights_dtype == MOE_DTYPE_BF16 || weights_dtype == MOE_DTYPE_F32, MOE_ERR_DTYPE,
               "%s: weights dtype %d", who, weights_dtype);
-  MOE_REQUIRE(offsets && out && (T == 0 || (y && slot && topk_weights)), MOE_ERR_ARG,
+  MOE_REQUIRE(offsets && (T == 0 || (out && y && slot && topk_weights)), MOE_ERR_ARG,
               "%s: null pointer", who);
   MOE_REQUIRE(al16(out) && (T == 0 || al16(y)), MOE_ERR_ALIGN, "%s: misaligned pointer", who);
   if (T == 0) return MOE_OK;
@@ -402,7 +402,7 @@ int gather_backward_impl(const void* d_xs, const int32_t* slot, const int32_t* o
                          void* stream, const char* who) {
   int rc = check_rows(T, K, E, H, dtype, who);
   if (rc) return rc;
-  MOE_REQUIRE(offsets && d_x && (T == 0 || (d_xs && slot)), MOE_ERR_ARG, "%s: null pointer",
+  MOE_REQUIRE(offsets && (T == 0 || (d_x && d_xs && slot)), MOE_ERR_ARG, "%s: null pointer",
               who);
   MOE_REQUIRE(al16(d_x) && (T == 0 || al16(d_xs)) && (!addend || al16(addend)), MOE_ERR_ALIGN,
               "%s: misaligned pointer", who);
@@ -428,7 +428,7 @@ extern "C" int moe_amd_gather_backward_add(const void* d_xs, const int32_t* slot
                                            const int32_t* offsets, const void* addend, int64_t T,
                                            int K, int E, int H, int dtype, void* d_x,
                                            void* stream) {
-  MOE_REQUIRE(addend, MOE_ERR_ARG, "gather_backward_add: null addend");
+  MOE_REQUIRE(addend || T == 0, MOE_ERR_ARG, "gather_backward_add: null addend");
   return gather_backward_impl(d_xs, slot, offsets, addend, T, K, E, H, dtype, d_x, stream,
                               "gather_backward_add");
 }

@@ -1039,7 +1039,7 @@ extern "C" int moe_amd_gemm_gate_up_swiglu(const void* hidden_states, const int3
   MOE_REQUIRE(top_k >= 1 && S == T * top_k, MOE_ERR_ARG, "%s: S != T*top_k", who);
   MOE_REQUIRE(T * (int64_t)H * 2 < ((int64_t)1 << 31), MOE_ERR_UNSUPPORTED, "%s: T*H too large",
               who);
-  MOE_REQUIRE(hidden_states && row_src && offsets && tile_plan && gate_up_proj && act_out,
+  MOE_REQUIRE(offsets && tile_plan && gate_up_proj && (S == 0 || (hidden_states && row_src && act_out)),
               MOE_ERR_ARG, "%s: null pointer", who);
   MOE_ALIGNED(hidden_states, who);
   MOE_ALIGNED(gate_up_proj, who);
@@ -1063,7 +1063,7 @@ extern "C" int moe_amd_gemm_down(const void* act, const int32_t* offsets,
   const char* who = "gemm_down";
   int rc = check_common(S, E, H, I, dtype, who);
   if (rc) return rc;
-  MOE_REQUIRE(act && offsets && tile_plan && down_proj && y_out, MOE_ERR_ARG,
+  MOE_REQUIRE(offsets && tile_plan && down_proj && (S == 0 || (act && y_out)), MOE_ERR_ARG,
               "%s: null pointer", who);
   MOE_ALIGNED(act, who);
   MOE_ALIGNED(down_proj, who);
@@ -1217,8 +1217,8 @@ extern "C" int moe_amd_gemm_down_backward_dx_dswiglu(const void* dy, const int32
   const char* who = "gemm_down_backward_dx_dswiglu";
   int rc = check_common(S, E, H, I, dtype, who);
   if (rc) return rc;
-  MOE_REQUIRE(dy && offsets && tile_plan && down_proj && gate_up && d_gate_up, MOE_ERR_ARG,
-              "%s: null pointer", who);
+  MOE_REQUIRE(offsets && tile_plan && down_proj && (S == 0 || (dy && gate_up && d_gate_up)),
+              MOE_ERR_ARG, "%s: null pointer", who);
   MOE_ALIGNED(dy, who);
   MOE_ALIGNED(down_proj, who);
   MOE_ALIGNED(gate_up, who);
@@ -1249,8 +1249,9 @@ extern "C" int moe_amd_gemm_down_backward_dx_fused(
               who);
   MOE_REQUIRE(weights_dtype == MOE_DTYPE_F32 || weights_dtype == MOE_DTYPE_BF16, MOE_ERR_ARG,
               "%s: weights_dtype must be fp32 or bf16", who);
-  MOE_REQUIRE(d_out && row_src && offsets && tile_plan && down_proj && gate_up && topk_weights &&
-                  d_gate_up && act_w && dw_partials,
+  MOE_REQUIRE(offsets && tile_plan && down_proj &&
+                  (S == 0 || (d_out && row_src && gate_up && topk_weights && d_gate_up && act_w &&
+                              dw_partials)),
               MOE_ERR_ARG, "%s: null pointer", who);
   MOE_ALIGNED(d_out, who);
   MOE_ALIGNED(down_proj, who);
@@ -1281,7 +1282,7 @@ extern "C" int moe_amd_gemm_gate_up_backward_dx(const void* d_gate_up, const int
   const char* who = "gemm_gate_up_backward_dx";
   int rc = check_common(S, E, H, I, dtype, who);
   if (rc) return rc;
-  MOE_REQUIRE(d_gate_up && offsets && tile_plan && gate_up_proj && d_xs, MOE_ERR_ARG,
+  MOE_REQUIRE(offsets && tile_plan && gate_up_proj && (S == 0 || (d_gate_up && d_xs)), MOE_ERR_ARG,
               "%s: null pointer", who);
   MOE_ALIGNED(d_gate_up, who);
   MOE_ALIGNED(gate_up_proj, who);

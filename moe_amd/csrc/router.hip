@@ -381,7 +381,7 @@ extern "C" int moe_amd_router_softmax_topk(const void* logits, int logits_dtype,
   if (rc) return rc;
   MOE_REQUIRE(logits_dtype == MOE_DTYPE_F32 || logits_dtype == MOE_DTYPE_BF16, MOE_ERR_DTYPE,
               "router_softmax_topk: logits dtype %d", logits_dtype);
-  MOE_REQUIRE(logits && probs && topk_weights && topk_index, MOE_ERR_ARG,
+  MOE_REQUIRE(T == 0 || (logits && probs && topk_weights && topk_index), MOE_ERR_ARG,
               "router_softmax_topk: null pointer");
   if (T == 0) return MOE_OK;
   size_t shm = tokens_per_expert ? (size_t)E * sizeof(int) : 0;
@@ -401,7 +401,7 @@ extern "C" int moe_amd_router_softmax_topk_backward(const float* probs, const in
   if (rc) return rc;
   MOE_REQUIRE(d_logits_dtype == MOE_DTYPE_F32 || d_logits_dtype == MOE_DTYPE_BF16,
               MOE_ERR_DTYPE, "router_softmax_topk_backward: dtype %d", d_logits_dtype);
-  MOE_REQUIRE(probs && topk_index && d_topk_weights && d_logits, MOE_ERR_ARG,
+  MOE_REQUIRE(T == 0 || (probs && topk_index && d_topk_weights && d_logits), MOE_ERR_ARG,
               "router_softmax_topk_backward: null pointer");
   if (T == 0) return MOE_OK;
   MOE_DISPATCH_NV(E, softmax_topk_bwd_kernel, grid_for(T), 64 * kWavesPerBlock, 0,
@@ -420,7 +420,7 @@ extern "C" int moe_amd_router_sigmoid_topk(const float* logits, const float* exp
   if (rc) return rc;
   MOE_REQUIRE(weights_dtype == MOE_DTYPE_F32 || weights_dtype == MOE_DTYPE_BF16, MOE_ERR_DTYPE,
               "router_sigmoid_topk: weights dtype %d", weights_dtype);
-  MOE_REQUIRE(logits && scores && topk_weights && topk_index, MOE_ERR_ARG,
+  MOE_REQUIRE(T == 0 || (logits && scores && topk_weights && topk_index), MOE_ERR_ARG,
               "router_sigmoid_topk: null pointer");
   if (num_groups > 0) {
     MOE_REQUIRE(num_groups <= 64 && E % num_groups == 0 && group_topk >= 1 &&
@@ -460,7 +460,7 @@ extern "C" int moe_amd_router_sigmoid_topk_backward(const float* scores,
   if (rc) return rc;
   MOE_REQUIRE(weights_dtype == MOE_DTYPE_F32 || weights_dtype == MOE_DTYPE_BF16, MOE_ERR_DTYPE,
               "router_sigmoid_topk_backward: weights dtype %d", weights_dtype);
-  MOE_REQUIRE(scores && topk_index && d_topk_weights && d_logits, MOE_ERR_ARG,
+  MOE_REQUIRE(T == 0 || (scores && topk_index && d_topk_weights && d_logits), MOE_ERR_ARG,
               "router_sigmoid_topk_backward: null pointer");
   if (T == 0) return MOE_OK;
   if (!(scaling_factor > 0.f)) scaling_factor = 0.f;

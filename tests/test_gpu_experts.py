@@ -347,3 +347,33 @@ def test_dw_schedule_matches_static_walk(T, H, E, K, I, skew):
     counts = plan.counts.cpu().numpy()
     load = [counts[xorder[xstart[i]:xstart[i + 1]]].sum() for i in range(8)]
     assert max(load) <= sum(load) / 8 + counts.max() + 1   # serpentine dealing bound
+
+
+@pytest.mark.parametrize("path", ["experts", "softmax_layer", "sigmoid_layer"])
+def test_zero_tokens(path):
+    """An empty batch (T = 0) runs through every op of the path, forward and
+    backward: empty outputs and input gradients, zero weight gradients."""
+    print(f"zero tokens {path}", flush=True)
+    H, E, K, I = 256, 16, 4, 128
+    g = torch.Generator().manual_seed(5)
+    bf = torch.bfloat16
+    x = torch.zeros(0, H, dtype=bf, device=DEV, requires_grad=True)
+    wr = (torch.randn(E, H, generator=g) * 0.02).to(bf).to(DEV).requires_grad_(True)
+    w1 = (torch.randn(E, 2 * I, H, generator=g) * 0.02).to(bf).to(DEV).requires_grad_(True)
+    w2 = (torch.randn(E, H, I, generator=g) * 0.02).to(bf).to(DEV).requires_grad_(True)
+    if path == "experts":
+        w = torch.zeros(0, K, device=DEV, requires_grad=True)
+        out = experts_forward(x, torch.zeros(0, K, dtype=torch.int64, device=DEV), w, w1, w2)
+    elif path == "softmax_layer":
+        out, probs, w, idx = moe_layer(x, wr, w1, w2, K)
+        assert probs.shape == (0, E) and idx.shape == (0, K)
+    else:
+        bias = torch.zeros(E, device=DEV)
+        out, probs, w, idx = moe_layer(x, wr, w1, w2, K, router="sigmoid", expert_bias=bias,
+                                       gating="hip")
+    out.backward(torch.zeros(0, H, dtype=bf, device=DEV))
+    torch.cuda.synchronize()
+    assert out.shape == (0, H) and x.grad.shape == (0, H)
+    assert not w1.grad.any() and not w2.grad.any()
+    if path != "experts":
+        assert wr.grad is None or not wr.grad.any()
