@@ -109,6 +109,164 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void softmax_topk_kernel(
   }
 }
 
+// The same softmax router for E <= 16*G experts and K <= G: G lanes per
+// token (64/G tokens per wave), V consecutive experts per lane, ranks through
+// rank_key with G-lane DPP butterflies.  Per token this takes about a fifth
+// of the VALU instructions of the wave-per-token kernel, which at E = 128 is
+// VALU-bound (64-lane reductions repeated K times for 2 values per lane).
+// Same arithmetic: probs = exp(v - max) / sum with the sum over the group in
+// a fixed butterfly order; the selected weights are those probs (recomputed
+// bit-identically from the winning key), renormalised by their sum in rank
+// order.
+template <int G, int V, bool KEY16, bool VEC>
+__global__ __launch_bounds__(64 * kWavesPerBlock) void softmax_topk_group_kernel(
+    const void* __restrict__ logits, int logits_dtype, const float* __restrict__ offset,
+    int64_t T, int E, int K, int renorm, float* __restrict__ probs, float* __restrict__ topk_w,
+    int64_t* __restrict__ topk_idx, float* __restrict__ tpe) {
+  // KEY16: bf16 logits without offset, ranked by 32-bit keys from the bf16
+  // bits; otherwise 64-bit keys from the fp32 values.  VEC: E == G*V (every
+  // lane owns V real experts), so a lane's logits and probs move as 16-byte
+  // vectors (a token's row is contiguous across its G lanes).
+  using Key = std::conditional_t<KEY16, uint32_t, uint64_t>;
+  extern __shared__ int hist[];  // [E] when tpe != nullptr
+  constexpr int TPW = 64 / G;    // tokens per wave
+  const int lane = threadIdx.x & 63, g = lane & (G - 1), sub = lane / G;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (tpe) {
+    for (int e = threadIdx.x; e < E; e += blockDim.x) hist[e] = 0;
+    __syncthreads();
+  }
+  const int e0 = g * V;
+  const int64_t stride = (int64_t)gridDim.x * kWavesPerBlock * TPW;
+  for (int64_t tb = ((int64_t)blockIdx.x * kWavesPerBlock + wid) * TPW; tb < T; tb += stride) {
+    const int64_t t = tb + sub;
+    const bool tok = t < T;
+    float v[V];
+    Key key[V];
+    if constexpr (VEC && KEY16) {
+      static_assert(V % 8 == 0, "16-byte bf16 vectors");
+      const u32x4* src = (const u32x4*)((const uint16_t*)logits + (tok ? t : 0) * E + e0);
+#pragma unroll
+      for (int q = 0; q < V / 8; ++q) {
+        const u32x4 w = tok ? src[q] : u32x4{0xff80ff80u, 0xff80ff80u, 0xff80ff80u, 0xff80ff80u};
+#pragma unroll
+        for (int h = 0; h < 8; ++h) {
+          const uint32_t bits = (w[h >> 1] >> (16 * (h & 1))) & 0xffffu;
+          v[q * 8 + h] = __uint_as_float(bits << 16);
+          key[q * 8 + h] = rank_key16(bits, e0 + q * 8 + h);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        const int e = e0 + j;
+        const bool in = tok && e < E;
+        if constexpr (KEY16) {
+          const uint32_t bits = in ? (uint32_t)((const uint16_t*)logits)[t * E + e] : 0xff80u;
+          v[j] = __uint_as_float(bits << 16);  // -inf outside the row
+          key[j] = e < E ? rank_key16(bits, e) : 0u;
+        } else {
+          v[j] = in ? load_logit(logits, logits_dtype, t * E + e) + (offset ? offset[e] : 0.f)
+                    : -INFINITY;
+          key[j] = e < E ? rank_key(v[j], e) : 0ull;
+        }
+      }
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < V; ++j) m = fmaxf(m, v[j]);
+    m = group_max<G>(m);
+    float p[V];
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      p[j] = (e0 + j < E) ? expf(v[j] - m) : 0.f;
+      s += p[j];
+    }
+    s = group_sum<G>(s);
+    if constexpr (VEC) {
+      if (tok) {
+        f32x4* dst = (f32x4*)(probs + t * E + e0);
+#pragma unroll
+        for (int q = 0; q < V / 4; ++q)
+          dst[q] = f32x4{p[4 * q] / s, p[4 * q + 1] / s, p[4 * q + 2] / s, p[4 * q + 3] / s};
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        const int e = e0 + j;
+        if (tok && e < E) probs[t * E + e] = p[j] / s;
+      }
+    }
+    float my_w = 0.f, ssum = 0.f;
+    int my_e = 0;
+    for (int k = 0; k < K; ++k) {
+      Key b = key[0];
+#pragma unroll
+      for (int j = 1; j < V; ++j) b = key[j] > b ? key[j] : b;
+      b = group_max_key<G>(b);
+#pragma unroll
+      for (int j = 0; j < V; ++j) key[j] = key[j] == b ? 0 : key[j];
+      const float pe = expf(key_value(b) - m) / s;  // == probs of the winner
+      ssum += pe;
+      if (g == k) {
+        my_w = pe;
+        my_e = key_index(b);
+      }
+    }
+    if (renorm) my_w = my_w / ssum;
+    if (tok && g < K) {
+      topk_w[t * K + g] = my_w;
+      topk_idx[t * K + g] = my_e;
+      if (tpe) atomicAdd(&hist[my_e], 1);
+    }
+  }
+  if (tpe) {
+    __syncthreads();
+    for (int e = threadIdx.x; e < E; e += blockDim.x)
+      if (hist[e]) atomicAdd(&tpe[e], (float)hist[e]);
+  }
+}
+
+// Lanes per token and experts per lane of the group kernels, or G = 0 when
+// E and K call for the wave-per-token kernels.
+void group_shape(int E, int K, int& G, int& V) {
+  G = K <= 8 ? 8 : (K <= 16 ? 16 : 0);
+  if (G == 8 && E > 8 * 16) G = 16;
+  if (G == 0 || E > G * 16) {
+    G = 0;
+    return;
+  }
+  const int need = (E + G - 1) / G;
+  V = need <= 4 ? 4 : (need <= 8 ? 8 : 16);
+}
+// The group kernel's variants: 32-bit keys for bf16 logits without offset,
+// 16-byte vectors when the experts fill the G lanes exactly.
+template <int G, int V>
+void launch_softmax_group(bool key16, int grid, size_t shm, hipStream_t st, const void* logits,
+                          int dtype, const float* offset, int64_t T, int E, int K, int renorm,
+                          float* probs, float* w, int64_t* idx, float* tpe) {
+#define MOE_GROUP_LAUNCH(K16, VEC)                                                         \
+  softmax_topk_group_kernel<G, V, K16, VEC><<<grid, 64 * kWavesPerBlock, shm, st>>>(        \
+      logits, dtype, offset, T, E, K, renorm, probs, w, idx, tpe)
+  if constexpr (V % 8 == 0) {
+    if (E == G * V) {
+      if (key16) MOE_GROUP_LAUNCH(true, true);
+      else MOE_GROUP_LAUNCH(false, true);
+      return;
+    }
+  }
+  if (key16) MOE_GROUP_LAUNCH(true, false);
+  else MOE_GROUP_LAUNCH(false, false);
+#undef MOE_GROUP_LAUNCH
+}
+int grid_group(int64_t T, int G) {
+  const int64_t per_block = (int64_t)kWavesPerBlock * (64 / G) * 2;  // two token batches per wave
+  int64_t blocks = (T + per_block - 1) / per_block;
+  if (blocks > 8192) blocks = 8192;
+  return (int)(blocks < 1 ? 1 : blocks);
+}
+
 template <int NV, bool GROUPS>
 __global__ __launch_bounds__(64 * kWavesPerBlock) void sigmoid_topk_kernel(
     const float* __restrict__ logits, const float* __restrict__ bias, int64_t T, int E, int K,
@@ -385,10 +543,25 @@ extern "C" int moe_amd_router_softmax_topk(const void* logits, int logits_dtype,
               "router_softmax_topk: null pointer");
   if (T == 0) return MOE_OK;
   size_t shm = tokens_per_expert ? (size_t)E * sizeof(int) : 0;
-  MOE_DISPATCH_NV(E, softmax_topk_kernel, grid_fwd(T), 64 * kWavesPerBlock, shm,
-                  (hipStream_t)stream >>>(logits, logits_dtype, logit_offset, T, E, K,
-                                          renormalize, probs, topk_weights, topk_index,
-                                          tokens_per_expert));
+  int G, V;
+  group_shape(E, K, G, V);
+  hipStream_t st = (hipStream_t)stream;
+#define MOE_SOFTMAX_GROUP(G_, V_)                                                     \
+  launch_softmax_group<G_, V_>(key16, grid_group(T, G_), shm, st, logits, logits_dtype, \
+                               logit_offset, T, E, K, renormalize, probs, topk_weights,  \
+                               topk_index, tokens_per_expert)
+  const bool key16 = logits_dtype == MOE_DTYPE_BF16 && !logit_offset;
+  if (G == 8 && V == 4) MOE_SOFTMAX_GROUP(8, 4);
+  else if (G == 8 && V == 8) MOE_SOFTMAX_GROUP(8, 8);
+  else if (G == 8) MOE_SOFTMAX_GROUP(8, 16);
+  else if (G == 16 && V == 4) MOE_SOFTMAX_GROUP(16, 4);
+  else if (G == 16 && V == 8) MOE_SOFTMAX_GROUP(16, 8);
+  else if (G == 16) MOE_SOFTMAX_GROUP(16, 16);
+  else
+    MOE_DISPATCH_NV(E, softmax_topk_kernel, grid_fwd(T), 64 * kWavesPerBlock, shm,
+                    st >>>(logits, logits_dtype, logit_offset, T, E, K, renormalize, probs,
+                           topk_weights, topk_index, tokens_per_expert));
+#undef MOE_SOFTMAX_GROUP
   return check_launch("router_softmax_topk");
 }
 

@@ -3,6 +3,8 @@
 // of lane L being entry j*64 + L; entries rank by value, descending, and
 // equal values by lower index.
 #pragma once
+#include <type_traits>
+
 #include "common.h"
 
 namespace moe {
@@ -76,6 +78,88 @@ __device__ __forceinline__ int wave_topk(const float (&val)[NV], uint64_t taken,
     if ((be & 63) == lane) taken |= 1ull << (be >> 6);
   }
   return mine;
+}
+
+// ---------------------------------------------------------------------------
+// Group top-k: G = 8 or 16 consecutive lanes own one row (64/G rows per
+// wave), V entries per lane (entries g*V .. g*V+V-1 of lane g of the group).
+// Entries are ranked through one ordered 64-bit key each, (value mapped to
+// an unsigned order) << 32 | (2^32 - 1 - index): larger key = ranks first,
+// so a single unsigned max implements "value descending, lower index on
+// equal values".  -0 is folded into +0 first (equal values compare by index
+// only); a NaN maps above every number (as in torch.topk).
+__device__ __forceinline__ uint64_t rank_key(float v, int idx) {
+  uint32_t b = __float_as_uint(v + 0.0f);
+  b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return ((uint64_t)b << 32) | (uint32_t)(0xffffffffu - (uint32_t)idx);
+}
+__device__ __forceinline__ float key_value(uint64_t k) {
+  uint32_t b = (uint32_t)(k >> 32);
+  b = (b & 0x80000000u) ? (b & 0x7fffffffu) : ~b;
+  return __uint_as_float(b);
+}
+__device__ __forceinline__ int key_index(uint64_t k) {
+  return (int)(0xffffffffu - (uint32_t)k);
+}
+
+// One butterfly step within rows of 16 lanes (every source lane is valid).
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, CTRL, 0xF, 0xF, true);
+}
+// The steps that combine G consecutive lanes (G = 2, 4, 8, 16): quad xor 1,
+// quad xor 2, half-row mirror (lane i <-> 7-i of each 8), row mirror (lane
+// i <-> 15-i of each 16).  Both partners of a step compute op(a, b) of the
+// same two values, so every lane of the group ends with the same result.
+template <int G, typename F>
+__device__ __forceinline__ void group_steps(F&& step) {
+  if constexpr (G >= 2) step(std::integral_constant<int, 0xB1>{});
+  if constexpr (G >= 4) step(std::integral_constant<int, 0x4E>{});
+  if constexpr (G >= 8) step(std::integral_constant<int, 0x141>{});
+  if constexpr (G >= 16) step(std::integral_constant<int, 0x140>{});
+}
+// 32-bit form for bf16 values and indices below 2^16: the same order from
+// the bf16 bits (value exact), one unsigned max per comparison.
+__device__ __forceinline__ uint32_t rank_key16(uint32_t bf_bits, int idx) {
+  uint32_t b = bf_bits == 0x8000u ? 0u : bf_bits;  // -0 -> +0
+  b = (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
+  return (b << 16) | (0xffffu - (uint32_t)idx);
+}
+__device__ __forceinline__ float key_value(uint32_t k) {
+  uint32_t b = k >> 16;
+  b = (b & 0x8000u) ? (b & 0x7fffu) : (~b & 0xffffu);
+  return __uint_as_float(b << 16);
+}
+__device__ __forceinline__ int key_index(uint32_t k) { return (int)(0xffffu - (k & 0xffffu)); }
+template <int G>
+__device__ __forceinline__ uint32_t group_max_key(uint32_t k) {
+  group_steps<G>([&](auto c) {
+    const uint32_t o = dpp_u32<decltype(c)::value>(k);
+    k = o > k ? o : k;
+  });
+  return k;
+}
+template <int G>
+__device__ __forceinline__ uint64_t group_max_key(uint64_t k) {
+  group_steps<G>([&](auto c) {
+    constexpr int CTRL = decltype(c)::value;
+    const uint64_t o = ((uint64_t)dpp_u32<CTRL>((uint32_t)(k >> 32)) << 32) |
+                       dpp_u32<CTRL>((uint32_t)k);
+    k = o > k ? o : k;
+  });
+  return k;
+}
+template <int G>
+__device__ __forceinline__ float group_max(float v) {
+  group_steps<G>([&](auto c) {
+    v = fmaxf(v, __uint_as_float(dpp_u32<decltype(c)::value>(__float_as_uint(v))));
+  });
+  return v;
+}
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+  group_steps<G>([&](auto c) { v += __uint_as_float(dpp_u32<decltype(c)::value>(__float_as_uint(v))); });
+  return v;
 }
 
 }  // namespace moe

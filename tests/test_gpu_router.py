@@ -29,6 +29,8 @@ def _rel(a, b):
     (8192, 2048, 128, 8, torch.bfloat16),    # L / M shape (token sample)
     (512, 256, 1792, 8, torch.bfloat16),     # retrofit expert count
     (333, 128, 60, 6, torch.bfloat16),       # ragged sizes
+    (1000, 256, 256, 12, torch.bfloat16),    # 16 lanes per token, K > 8
+    (777, 128, 200, 8, torch.bfloat16),      # 16 lanes per token, partly empty lanes
 ])
 def test_softmax_router_parity(T, H, E, K, dtype):
     print(f"softmax router T={T} H={H} E={E} K={K} {dtype}", flush=True)
