@@ -308,7 +308,6 @@ int check_rows(int64_t T, int K, int E, int H, int dtype, const char* who) {
   return MOE_OK;
 }
 
-bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 // Launches KERNEL<T, KM> with KM = K for the common top-k values, else the
 // any-K form (KM = 0).

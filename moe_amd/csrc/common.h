@@ -59,6 +59,9 @@ static inline size_t plan_bytes(int64_t S, int E) {
   return plan_sched_offset(S, E) + align_up((size_t)(kSchedQueueInts + kSchedStartInts + E) * 4, 16);
 }
 
+// True for a null or 16-byte aligned pointer (the vector paths' requirement).
+static inline bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
 // ---- bf16 helpers -------------------------------------------------------
 // Conversions go through clang's __bf16 type, which rounds to nearest-even
 // (the same rounding torch applies when it stores an fp32 result as bf16).

@@ -250,7 +250,7 @@ void launch_softmax_group(bool key16, int grid, size_t shm, hipStream_t st, cons
   softmax_topk_group_kernel<G, V, K16, VEC><<<grid, 64 * kWavesPerBlock, shm, st>>>(        \
       logits, dtype, offset, T, E, K, renorm, probs, w, idx, tpe)
   if constexpr (V % 8 == 0) {
-    if (E == G * V) {
+    if (E == G * V && al16(logits) && al16(probs)) {
       if (key16) MOE_GROUP_LAUNCH(true, true);
       else MOE_GROUP_LAUNCH(false, true);
       return;
@@ -389,6 +389,83 @@ __device__ __forceinline__ float renorm_backward(float vk, float gk, int K, floa
   }
   float den = ssum + eps;
   return gk / den - gv / (den * den);
+}
+
+// The softmax router's backward for E == G*V (V a multiple of 8) and K <= G:
+// G lanes per token as in the forward group kernel, rows moved as 16-byte
+// vectors, the K routed (expert, gradient) pairs broadcast from the group's
+// lanes k < K in rank order (same sums as renorm_backward).
+template <int G, int V>
+__global__ __launch_bounds__(64 * kWavesPerBlock) void softmax_topk_bwd_group_kernel(
+    const float* __restrict__ probs, const int64_t* __restrict__ idx,
+    const float* __restrict__ dw, const float* __restrict__ dprobs, int64_t T, int E, int K,
+    int renorm, void* __restrict__ dlogits, int dl_dtype) {
+  static_assert(V % 8 == 0, "16-byte vectors");
+  constexpr int TPW = 64 / G;
+  const int lane = threadIdx.x & 63, g = lane & (G - 1), base = lane - g, sub = lane / G;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int e0 = g * V;
+  const int64_t stride = (int64_t)gridDim.x * kWavesPerBlock * TPW;
+  for (int64_t tb = ((int64_t)blockIdx.x * kWavesPerBlock + wid) * TPW; tb < T; tb += stride) {
+    const int64_t t = tb + sub;
+    const bool tok = t < T;
+    const int64_t tt = tok ? t : T - 1;  // rows past T load a valid row and store nothing
+    const int ek = g < K ? (int)idx[tt * K + g] : 0;
+    const float gk = g < K ? dw[tt * K + g] : 0.f;
+    const float vk = g < K ? probs[tt * E + ek] : 0.f;
+    float dv = gk;
+    if (renorm) {
+      float ssum = 0.f, gv = 0.f;
+      for (int k = 0; k < K; ++k) {
+        ssum += __shfl(vk, base + k, 64);
+        gv += __shfl(gk * vk, base + k, 64);
+      }
+      dv = gk / ssum - gv / (ssum * ssum);
+    }
+    float p[V], dp[V];
+    const f32x4* prow = (const f32x4*)(probs + tt * E + e0);
+#pragma unroll
+    for (int q = 0; q < V / 4; ++q) {
+      const f32x4 a = prow[q];
+      const f32x4 d = dprobs ? ((const f32x4*)(dprobs + tt * E + e0))[q] : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        p[4 * q + h] = a[h];
+        dp[4 * q + h] = d[h];
+      }
+    }
+    for (int k = 0; k < K; ++k) {
+      const int e = __shfl(ek, base + k, 64);
+      const float gg = __shfl(dv, base + k, 64);
+#pragma unroll
+      for (int j = 0; j < V; ++j)
+        if (e == e0 + j) dp[j] += gg;
+    }
+    float dot = 0.f;
+#pragma unroll
+    for (int j = 0; j < V; ++j) dot += p[j] * dp[j];
+    dot = group_sum<G>(dot);
+    if (!tok) continue;
+    if (dl_dtype == MOE_DTYPE_BF16) {
+      u32x4* out = (u32x4*)((bf16*)dlogits + t * E + e0);
+#pragma unroll
+      for (int q = 0; q < V / 8; ++q) {
+        u32x4 w;
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          const int j = 8 * q + 2 * h;
+          w[h] = pack_bf2((dp[j] - dot) * p[j], (dp[j + 1] - dot) * p[j + 1]);
+        }
+        out[q] = w;
+      }
+    } else {
+      f32x4* out = (f32x4*)((float*)dlogits + t * E + e0);
+#pragma unroll
+      for (int q = 0; q < V / 4; ++q)
+        out[q] = f32x4{(dp[4 * q] - dot) * p[4 * q], (dp[4 * q + 1] - dot) * p[4 * q + 1],
+                       (dp[4 * q + 2] - dot) * p[4 * q + 2], (dp[4 * q + 3] - dot) * p[4 * q + 3]};
+    }
+  }
 }
 
 template <int NV>
@@ -577,6 +654,20 @@ extern "C" int moe_amd_router_softmax_topk_backward(const float* probs, const in
   MOE_REQUIRE(T == 0 || (probs && topk_index && d_topk_weights && d_logits), MOE_ERR_ARG,
               "router_softmax_topk_backward: null pointer");
   if (T == 0) return MOE_OK;
+  int G, V;
+  group_shape(E, K, G, V);
+  if (G && E == G * V && V % 8 == 0 && al16(probs) && al16(d_probs) && al16(d_logits)) {
+    hipStream_t st = (hipStream_t)stream;
+#define MOE_BWD_GROUP(G_, V_)                                                               \
+  softmax_topk_bwd_group_kernel<G_, V_><<<grid_group(T, G_), 64 * kWavesPerBlock, 0, st>>>( \
+      probs, topk_index, d_topk_weights, d_probs, T, E, K, renormalize, d_logits, d_logits_dtype)
+    if (G == 8 && V == 8) MOE_BWD_GROUP(8, 8);
+    else if (G == 8) MOE_BWD_GROUP(8, 16);
+    else if (V == 8) MOE_BWD_GROUP(16, 8);
+    else MOE_BWD_GROUP(16, 16);
+#undef MOE_BWD_GROUP
+    return check_launch("router_softmax_topk_backward");
+  }
   MOE_DISPATCH_NV(E, softmax_topk_bwd_kernel, grid_for(T), 64 * kWavesPerBlock, 0,
                   (hipStream_t)stream >>>(probs, topk_index, d_topk_weights, d_probs, T, E, K,
                                           renormalize, d_logits, d_logits_dtype));

@@ -131,14 +131,20 @@ def test_sigmoid_router_no_nan_at_zero_scores():
 
 
 @pytest.mark.parametrize("renorm", [True, False])
-def test_softmax_router_backward_parity(renorm):
-    g = torch.Generator().manual_seed(21)
-    T, E, K = 2048, 128, 8
+@pytest.mark.parametrize("E,K,with_dp", [(128, 8, True), (128, 8, False), (64, 6, True),
+                                         (256, 12, False), (60, 6, True)])
+def test_softmax_router_backward_parity(renorm, E, K, with_dp):
+    print(f"softmax router backward E={E} K={K} renorm={renorm} d_probs={with_dp}", flush=True)
+    g = torch.Generator().manual_seed(21 + E + K)
+    T = 2048 + 3
     logits = (torch.randn(T, E, generator=g)).to(torch.bfloat16).to(DEV).requires_grad_(True)
     probs, w, idx = softmax_topk(logits, K, renorm, None)
     dw = torch.randn(T, K, generator=g).to(DEV)
     dp = torch.randn(T, E, generator=g).to(DEV) * 0.1
-    (gl,) = torch.autograd.grad((w * dw).sum() + (probs * dp).sum(), logits)
+    if not with_dp:
+        dp = torch.zeros_like(dp)
+    loss = (w * dw).sum() + ((probs * dp).sum() if with_dp else 0)
+    (gl,) = torch.autograd.grad(loss, logits)
     ref = O.softmax_router_backward(probs.detach().cpu(), idx.cpu(), dw.cpu(), dp.cpu(), renorm,
                                     torch.float32)
     assert gl.dtype == torch.bfloat16
