@@ -58,6 +58,124 @@ __device__ void block_combine(const float (&acc)[NV], int E, float* buf, float* 
   }
 }
 
+// The same statistics with G lanes per token (E <= 16*G, K <= G): lane g of
+// a group owns experts g*V .. g*V+V-1, ranks through rank_key with G-lane DPP
+// butterflies (as the softmax router's group kernel).  The block partial is
+// the sum over the block's kWaves*64/G token groups in group order, through
+// LDS ([groups][E] floats, dynamic shared memory).
+template <int G, int V>
+__global__ __launch_bounds__(64 * kWaves) void topk_stats_group_kernel(
+    const void* __restrict__ probs, int dtype, const float* __restrict__ tok_w, int64_t T, int E,
+    int K, float* __restrict__ part_cnt, float* __restrict__ part_sum,
+    double* __restrict__ part_margin) {
+  constexpr int TPW = 64 / G, ROWS = kWaves * TPW;
+  extern __shared__ float sbuf[];  // [ROWS][E]
+  __shared__ double msh[ROWS], mmn[ROWS];
+  const int lane = threadIdx.x & 63, g = lane & (G - 1), sub = lane / G;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int row = wid * TPW + sub, e0 = g * V;
+  const bool vec = E == G * V && (dtype == MOE_DTYPE_F32 ? V % 4 == 0 : V % 8 == 0) &&
+                   (((uintptr_t)probs & 15) == 0);
+  float cnt[V], psum[V];
+#pragma unroll
+  for (int j = 0; j < V; ++j) cnt[j] = psum[j] = 0.f;
+  double msum = 0.0;
+  float mmin = INFINITY;
+  const int64_t stride = (int64_t)gridDim.x * kWaves * TPW;
+  for (int64_t tb = ((int64_t)blockIdx.x * kWaves + wid) * TPW; tb < T; tb += stride) {
+    const int64_t t = tb + sub;
+    const bool tok = t < T;
+    const int64_t tt = tok ? t : T - 1;
+    const float w = tok ? (tok_w ? tok_w[t] : 1.f) : 0.f;
+    float v[V];
+    if (vec) {
+      if (dtype == MOE_DTYPE_F32) {
+        const f32x4* src = (const f32x4*)((const float*)probs + tt * E + e0);
+#pragma unroll
+        for (int q = 0; q < V / 4; ++q) {
+          const f32x4 a = src[q];
+#pragma unroll
+          for (int h = 0; h < 4; ++h) v[4 * q + h] = a[h];
+        }
+      } else {
+        const u32x4* src = (const u32x4*)((const bf16*)probs + tt * E + e0);
+#pragma unroll
+        for (int q = 0; q < (V + 7) / 8; ++q) {
+          const u32x4 a = src[q];
+#pragma unroll
+          for (int h = 0; h < 8; ++h)
+            if (8 * q + h < V) v[8 * q + h] = (h & 1) ? bf_hi(a[h >> 1]) : bf_lo(a[h >> 1]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < V; ++j)
+        v[j] = e0 + j < E ? load_val(probs, dtype, tt * E + e0 + j) : -INFINITY;
+    }
+    uint64_t key[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      if (tok && e0 + j < E) psum[j] += w * v[j];
+      key[j] = e0 + j < E ? rank_key(v[j], e0 + j) : 0ull;
+    }
+    float vk = 0.f;  // value of the k-th selection
+    for (int k = 0; k < K; ++k) {
+      uint64_t b = key[0];
+#pragma unroll
+      for (int j = 1; j < V; ++j) b = key[j] > b ? key[j] : b;
+      b = group_max_key<G>(b);
+#pragma unroll
+      for (int j = 0; j < V; ++j) key[j] = key[j] == b ? 0ull : key[j];
+      vk = key_value(b);
+    }
+    if (tok) {
+#pragma unroll
+      for (int j = 0; j < V; ++j)
+        if (e0 + j < E && key[j] == 0ull) cnt[j] += w;  // selected (real keys are never 0)
+    }
+    if (K < E) {  // margin between the k-th and (k+1)-th largest value
+      uint64_t b = key[0];
+#pragma unroll
+      for (int j = 1; j < V; ++j) b = key[j] > b ? key[j] : b;
+      b = group_max_key<G>(b);
+      const float m = vk - key_value(b);
+      if (tok) {
+        msum += (double)m;
+        mmin = fminf(mmin, m);
+      }
+    }
+  }
+  // Block partials: rows in group order, per expert.
+  auto combine = [&](const float (&acc)[V], float* out) {
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < V; ++j)
+      if (e0 + j < E) sbuf[row * E + e0 + j] = acc[j];
+    __syncthreads();
+    for (int e = threadIdx.x; e < E; e += blockDim.x) {
+      float s = 0.f;
+      for (int r = 0; r < ROWS; ++r) s += sbuf[r * E + e];
+      out[e] = s;
+    }
+  };
+  combine(cnt, part_cnt + (size_t)blockIdx.x * E);
+  combine(psum, part_sum + (size_t)blockIdx.x * E);
+  if (g == 0) {
+    msh[row] = msum;
+    mmn[row] = (double)mmin;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double sm = 0.0, mn = INFINITY;
+    for (int r = 0; r < ROWS; ++r) {
+      sm += msh[r];
+      mn = fmin(mn, mmn[r]);
+    }
+    part_margin[blockIdx.x * 2] = sm;
+    part_margin[blockIdx.x * 2 + 1] = mn;
+  }
+}
+
 // One wave per token (grid-stride).  Per block: partial weighted selection
 // counts [E], weighted probability sums [E], and the margin sum and minimum.
 template <int NV>
@@ -465,8 +583,25 @@ extern "C" int moe_amd_topk_stats(const void* probs, int probs_dtype, const floa
     topk_stats_finalize_kernel<<<E + 1, 64, 0, st>>>(pc, ps, pm, 0, E, counts, prob_sums, margin);
     return check_launch(who);
   }
-  MOE_DISPATCH_NV_B(E, topk_stats_kernel, nb, 64 * kWaves, 0, st>>>(
-      probs, probs_dtype, token_weights, T, E, K, pc, ps, pm));
+  int G, V;
+  group_shape(E, K, G, V);
+  if (G) {
+    const size_t shm = (size_t)kWaves * (64 / G) * E * sizeof(float);
+#define MOE_STATS_GROUP(G_, V_)                                                        \
+  topk_stats_group_kernel<G_, V_><<<nb, 64 * kWaves, shm, st>>>(probs, probs_dtype,     \
+                                                                token_weights, T, E, K, \
+                                                                pc, ps, pm)
+    if (G == 8 && V == 4) MOE_STATS_GROUP(8, 4);
+    else if (G == 8 && V == 8) MOE_STATS_GROUP(8, 8);
+    else if (G == 8) MOE_STATS_GROUP(8, 16);
+    else if (V == 4) MOE_STATS_GROUP(16, 4);
+    else if (V == 8) MOE_STATS_GROUP(16, 8);
+    else MOE_STATS_GROUP(16, 16);
+#undef MOE_STATS_GROUP
+  } else {
+    MOE_DISPATCH_NV_B(E, topk_stats_kernel, nb, 64 * kWaves, 0, st>>>(
+        probs, probs_dtype, token_weights, T, E, K, pc, ps, pm));
+  }
   topk_stats_finalize_kernel<<<E + 1, 64, 0, st>>>(pc, ps, pm, nb, E, counts, prob_sums, margin);
   return check_launch(who);
 }

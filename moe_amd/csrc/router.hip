@@ -228,18 +228,6 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void softmax_topk_group_kernel
   }
 }
 
-// Lanes per token and experts per lane of the group kernels, or G = 0 when
-// E and K call for the wave-per-token kernels.
-void group_shape(int E, int K, int& G, int& V) {
-  G = K <= 8 ? 8 : (K <= 16 ? 16 : 0);
-  if (G == 8 && E > 8 * 16) G = 16;
-  if (G == 0 || E > G * 16) {
-    G = 0;
-    return;
-  }
-  const int need = (E + G - 1) / G;
-  V = need <= 4 ? 4 : (need <= 8 ? 8 : 16);
-}
 // The group kernel's variants: 32-bit keys for bf16 logits without offset,
 // 16-byte vectors when the experts fill the G lanes exactly.
 template <int G, int V>
@@ -260,6 +248,7 @@ void launch_softmax_group(bool key16, int grid, size_t shm, hipStream_t st, cons
   else MOE_GROUP_LAUNCH(false, false);
 #undef MOE_GROUP_LAUNCH
 }
+
 int grid_group(int64_t T, int G) {
   const int64_t per_block = (int64_t)kWavesPerBlock * (64 / G) * 2;  // two token batches per wave
   int64_t blocks = (T + per_block - 1) / per_block;

@@ -162,4 +162,16 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
+// Lanes per token and experts per lane of the group kernels, or G = 0 when
+// E and K call for the wave-per-token kernels.
+static inline void group_shape(int E, int K, int& G, int& V) {
+  G = K <= 8 ? 8 : (K <= 16 ? 16 : 0);
+  if (G == 8 && E > 8 * 16) G = 16;
+  if (G == 0 || E > G * 16) {
+    G = 0;
+    return;
+  }
+  const int need = (E + G - 1) / G;
+  V = need <= 4 ? 4 : (need <= 8 ? 8 : 16);
+}
 }  // namespace moe
