@@ -112,12 +112,15 @@ def copy_calibration(nbytes: int) -> None:
 # the same counters on a plain copy of known size (`--copy-calibration`); the
 # commands and per-counter figures are in profiles/gemm_hbm_traffic_L.md.
 RECORDED_TRAFFIC_L = {
-    "gemm_gate_up_swiglu": 10026612405,
-    "gemm_down": 5358301900,
-    "gemm_down_backward_dx_dswiglu": 7744586922,
-    "gemm_gate_up_backward_dx": 8175586656,
-    "gemm_down_backward_dw": 3921002086,
-    "gemm_gate_up_backward_dw": 6810623670,
+    "gemm_gate_up_swiglu": 9255388063,
+    "gemm_down": 5037341382,
+    "gemm_down_backward_dx_fused": 7960146801,
+    "gemm_down_backward_dw_gathered": 4621847096,
+    "gemm_gate_up_backward_dx": 8214588646,
+    "gemm_gate_up_backward_dw": 6875762976,
+    "router_linear": 302451347,
+    "router_linear_backward_dx": 289924521,
+    "router_linear_backward_dw": 318980091,
 }
 
 
