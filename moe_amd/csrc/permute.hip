@@ -7,10 +7,11 @@
 //   P2 scan      : per-expert exclusive scan over chunks (one block per
 //                  expert) + one block that scans the expert totals into
 //                  offsets and the per-tile-height GEMM tile prefixes.
-//   P3 scatter   : each wave replays its chunk 64 entries at a time; a
-//                  ballot loop groups lanes by expert, the in-wave rank is
-//                  the popcount of lower peers, and a per-wave LDS counter
-//                  carries the rank across rounds -> stable order.
+//   P3 scatter   : each wave replays its chunk 64 entries at a time; one
+//                  ballot per bit of the expert id groups the lanes by
+//                  expert (multi-split), the in-wave rank is the popcount of
+//                  lower peers, and a per-wave LDS counter carries the rank
+//                  across rounds -> stable order.
 // Ids outside [0,E) land in bin E (sentinels), after every real expert.
 #include "common.h"
 
@@ -78,7 +79,7 @@ __device__ int block_excl_scan(int v, int* tmp /* >= 16 ints */, int* total) {
 }
 
 // One block per bin e: exclusive scan of chunk_hist[e][0..nch) in place.
-__global__ __launch_bounds__(256) void chunk_scan_kernel(int* __restrict__ chunk_hist,
+__global__ __launch_bounds__(1024) void chunk_scan_kernel(int* __restrict__ chunk_hist,
                                                          int64_t nch, int* __restrict__ totals) {
   __shared__ int tmp[17];
   const int e = blockIdx.x;
@@ -208,21 +209,19 @@ __global__ __launch_bounds__(64 * kWaves) void scatter_kernel(
   __builtin_amdgcn_wave_barrier();
   if (c >= nch) return;
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  int key_bits = 1;  // bits of the largest key, E (sentinel bin)
+  while ((E >> key_bits) != 0) ++key_bits;
   const int64_t beg = c * kChunk;
   for (int i = 0; i < kChunk / 64; ++i) {
     const int64_t s = beg + i * 64 + lane;
     const bool valid = s < S;
     const int key = valid ? bin_of(ids[s], E) : -1;
-    // Group lanes by key: each pass peels off all lanes sharing the key of
-    // the lowest unassigned lane.
-    uint64_t todo = __ballot(valid);
-    uint64_t peers = 0;
-    while (todo) {
-      int leader = __builtin_ctzll(todo);
-      int lkey = __shfl(key, leader, 64);
-      uint64_t m = __ballot(key == lkey) & todo;
-      if (key == lkey) peers = m;
-      todo &= ~m;
+    // Lanes sharing this lane's key (multi-split by ballots): one ballot per
+    // key bit, each lane keeps the lanes that agree with it on that bit.
+    uint64_t peers = __ballot(valid);
+    for (int b = 0; b < key_bits; ++b) {
+      const uint64_t m = __ballot((key >> b) & 1);
+      peers &= ((key >> b) & 1) ? m : ~m;
     }
     int before = 0;
     if (valid) before = cnt[key];
@@ -283,7 +282,7 @@ extern "C" int moe_amd_permute(const int64_t* topk_index, int64_t S, int E, void
   if (nch > 0) {
     const int blocks = (int)((nch + kWaves - 1) / kWaves);
     hist_kernel<<<blocks, 64 * kWaves, lds, st>>>(topk_index, S, E, nch, chunk_hist);
-    chunk_scan_kernel<<<E + 1, 256, 0, st>>>(chunk_hist, nch, totals);
+    chunk_scan_kernel<<<E + 1, 1024, 0, st>>>(chunk_hist, nch, totals);
   }
   int* tile_starts = (int*)tile_plan;
   finalize_kernel<<<1, 1024, 0, st>>>(totals, nch > 0 ? 1 : 0, E, counts, offsets, tile_starts);
