@@ -75,6 +75,10 @@ constexpr int SROW = 260;  // bf16 per row of the epilogue staging tile (520 B: 
 
 // RL: the router's dense linear, logits[T, E] = x[T, H] . W_r[E, H]^T.
 // RDX: its input gradient, d_x[T, H] = d_logits[T, E] . W_r[E, H].
+// RLT: the same logits computed transposed, rows = experts (W_r, at most one
+//      or two row tiles) and columns = tokens, with the MFMA operands
+//      swapped so that the tile is stored as logits[T, E]: for E <= 128 a
+//      256-column tile of RL would be half padding.
 // RDW: its weight gradient split over token chunks c (split-K), fp32
 //      partial[c][E][H] = sum_{t in chunk c} d_logits[t, :]^T x[t, :].
 // G2DXF and G2DWG are the down GEMMs' backward fused with the combine's
@@ -84,7 +88,7 @@ constexpr int SROW = 260;  // bf16 per row of the epilogue staging tile (520 B: 
 // computes d_down_proj[e]^T = (w act)^T d_out[tokens] and stores it
 // transposed.
 enum Mode { G1F = 0, G2F = 1, G2DX = 2, G1DX = 3, G2DW = 4, G1DW = 5, RL = 6, RDX = 7, RDW = 8,
-            G2DXF = 9, G2DWG = 10 };
+            G2DXF = 9, G2DWG = 10, RLT = 11 };
 
 struct GemmArgs {
   const bf16* x;         // hidden_states [T,H]
@@ -206,14 +210,14 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
   constexpr int NW = kWaves<BR>;                          // waves, as NW/2 rows x 2 columns
   constexpr int NTHR = NW * 64;
   constexpr bool TOKEN = MODE <= G1DX || MODE == G2DXF;   // rows = routed rows of one expert
-  constexpr bool DENSE = MODE == RL || MODE == RDX;       // rows = all T tokens, one "expert"
-  constexpr bool COL_KM = !(MODE == G1F || MODE == G2F || MODE == RL);  // column operand k-major
+  constexpr bool DENSE = MODE == RL || MODE == RDX || MODE == RLT;  // one "expert", dense rows
+  constexpr bool COL_KM = !(MODE == G1F || MODE == G2F || MODE == RL || MODE == RLT);  // k-major cols
   constexpr bool ROW_KM = !TOKEN && !DENSE;               // row operand k-major (dW)
   constexpr bool DOWN_DX = MODE == G2DX || MODE == G2DXF;  // column operand down_proj[e], k-major
   constexpr bool GROW = MODE == G1F || MODE == G2DXF;      // row operand: token rows via row_src
   constexpr bool GCOL = MODE == G1DW || MODE == G2DWG;     // column operand: token rows via row_src (k-major)
   constexpr bool DW = MODE == G2DW || MODE == G1DW || MODE == G2DWG;
-  constexpr bool SWAP = MODE == G2DWG;  // MFMA operands swapped: lanes hold 4 consecutive rows
+  constexpr bool SWAP = MODE == G2DWG || MODE == RLT;  // MFMA operands swapped: lanes hold 4 consecutive rows
   constexpr int WR = BR / (NW / 2);                       // rows per wave
   constexpr int TJ = WR / 32;                             // MFMA row sub-tiles per wave
   constexpr int TI = 4;                                   // MFMA col sub-tiles per wave (128 cols)
@@ -287,7 +291,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       d.ct = tt % p.n_ct;
       d.e = 0;
       d.row0 = (tt / p.n_ct) * BR;
-      d.row_end = (int)min((int64_t)d.row0 + BR, p.T);
+      d.row_end = (int)min((int64_t)d.row0 + BR, MODE == RLT ? (int64_t)p.E : p.T);
       d.kbeg = d.kend = 0;
     } else {
       const int vi = tt / per_e;
@@ -314,7 +318,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
     d.kbeg = __builtin_amdgcn_readfirstlane(d.kbeg);
     d.kend = __builtin_amdgcn_readfirstlane(d.kend);
     int K_len;
-    if constexpr (MODE == G1F || DOWN_DX || MODE == RL) K_len = H;
+    if constexpr (MODE == G1F || DOWN_DX || MODE == RL || MODE == RLT) K_len = H;
     else if constexpr (MODE == RDX) K_len = p.E;
     else if constexpr (MODE == G2F) K_len = I;
     else if constexpr (MODE == G1DX) K_len = I2;
@@ -368,6 +372,17 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
         const int feat = d.ct * 128 + (f >> 7) * 64 + (lc & 63);
         const int wrow = (lc < 64) ? feat : I + feat;
         coff[i] = (uint32_t)wrow * (uint32_t)(H * 2) + kc_chunk(f) * 16;
+      }
+      cstep = BK * 2;
+    } else if constexpr (MODE == RLT) {
+      // hidden_states rows [T][H]: tokens are the tile's columns
+      cptr = (const char*)p.x;
+      cbytes = (uint32_t)(p.T * H * 2);
+#pragma unroll
+      for (int i = 0; i < CPW; ++i) {
+        const int f = kc_feature(wid + NW * i);
+        const int64_t tok = (int64_t)d.ct * BC + f;
+        coff[i] = tok < p.T ? (uint32_t)tok * (uint32_t)(H * 2) + kc_chunk(f) * 16 : kOOB;
       }
       cstep = BK * 2;
     } else if constexpr (MODE == G2F || MODE == RL) {
@@ -431,7 +446,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       }
       rstep = BK * 2;
     } else if constexpr (TOKEN || DENSE) {
-      const int ld = (MODE == G2F) ? I : ((MODE == G2DX || MODE == RL) ? H : (MODE == RDX ? p.E : I2));
+      const int ld = (MODE == G2F) ? I : ((MODE == G2DX || MODE == RL || MODE == RLT) ? H : (MODE == RDX ? p.E : I2));
       rptr = (const char*)(p.a0 + (int64_t)d.row0 * ld);
       rbytes = (uint32_t)((int64_t)(d.row_end - d.row0) * ld * 2);
 #pragma unroll
@@ -704,6 +719,28 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
 
     // --------------------------------------------------------- epilogue
     WAIT_VMCNT(0);    // no LDS DMA may still be landing in the stages
+    if constexpr (MODE == RLT) {
+      if (p.out_f32) {
+        // fp32 logits: with the operands swapped each lane holds 4
+        // consecutive experts of one token, stored as 16 bytes.
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+#pragma unroll
+          for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int e = cur.row0 + wr * WR + j * 32 + 8 * q + 4 * hl;
+              const int64_t t = (int64_t)cur.ct * BC + wc * 128 + i * 32 + l32;
+              if (t < p.T && e < cur.row_end) {
+                const f32x4 v = {acc[i][j][4 * q + 0], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                                 acc[i][j][4 * q + 3]};
+                *(f32x4*)(p.out_f32 + t * p.E + e) = v;
+              }
+            }
+        __syncthreads();  // every wave is done reading the k-stages
+        continue;
+      }
+    }
     if constexpr (MODE == RL || MODE == RDW) {
       if (p.out_f32) {
         // fp32 output (RL's logits, RDW's partials): each lane stores its
@@ -877,6 +914,18 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
           }
         }
       }
+    } else if constexpr (MODE == RLT) {
+      // bf16 logits from the transposed staging: BC token rows of BR
+      // experts; BR/8 lanes per row, 16 bytes each.
+      constexpr int LPR = BR / 8, RPP = NTHR / LPR;
+      const int c0 = (tid % LPR) * 8;
+      const int e = cur.row0 + c0;
+      for (int rr = tid / LPR; rr < BC; rr += RPP) {
+        const int64_t t = (int64_t)cur.ct * BC + rr;
+        if (t < p.T && e < p.E)
+          __builtin_nontemporal_store(*(const u32x4*)(stg + rr * SROW + c0),
+                                      (u32x4*)(p.out + t * p.E + e));
+      }
     } else {
       // Plain bf16 tile: y (G2F), d_xs (G1DX), d_down_proj (G2DW, G2DWG
       // from its transposed staging), d_gate_up_proj (G1DW).
@@ -889,8 +938,8 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
         ld = H;
         obase = p.out;
       } else if constexpr (DENSE) {
-        nrows = cur.row_end;
-        ld = MODE == RL ? p.E : H;
+        nrows = MODE == RLT ? (int)p.T : cur.row_end;  // RLT: rows of the stored tile are tokens
+        ld = (MODE == RL || MODE == RLT) ? p.E : H;
         obase = p.out;
       } else {
         constexpr bool DOWN = MODE == G2DW || MODE == G2DWG;
@@ -955,8 +1004,10 @@ int num_cus() {
 template <int MODE, int BR>
 int launch(const GemmArgs& a, int max_tiles, hipStream_t st) {
   constexpr size_t stages = (size_t)NSLOT * SLOT;
-  // staging tile, plus G2DXF's per-row weights and row_src
-  constexpr size_t staging = (size_t)BR * SROW * sizeof(bf16) + (MODE == G2DXF ? (size_t)BR * 8 : 0);
+  // staging tile ([BC][SROW] when transposed), plus G2DXF's per-row weights
+  // and row_src
+  constexpr size_t staging = (size_t)((MODE == G2DWG || MODE == RLT) ? BC : BR) * SROW * sizeof(bf16) +
+                             (MODE == G2DXF ? (size_t)BR * 8 : 0);
   const size_t lds = stages > staging ? stages : staging;
   if (max_tiles <= 0) return MOE_OK;
   hipError_t err = hipFuncSetAttribute((const void*)grouped_gemm_kernel<MODE, BR>,
@@ -1102,6 +1153,17 @@ extern "C" int moe_amd_router_linear(const void* hidden_states, const void* weig
   if (logits_dtype == MOE_DTYPE_F32) a.out_f32 = (float*)logits;
   else a.out = (bf16*)logits;
   a.T = T; a.E = E; a.H = H; a.I = 64;
+  if (E <= 256 && T * (int64_t)H * 2 < ((int64_t)1 << 31)) {
+    // Transposed (RLT): experts as rows, no padding columns for E < 256.
+    a.x = (const bf16*)hidden_states;
+    a.a0 = (const bf16*)weight;
+    a.n_ct = (int)((T + BC - 1) / BC);
+    a.n_rt = 1;
+    MOE_REQUIRE(a.n_ct < (1 << 30), MOE_ERR_UNSUPPORTED, "%s: too many tiles", who);
+    a.n_tiles = a.n_ct;
+    if (E <= 128) return launch<RLT, 128>(a, a.n_tiles, (hipStream_t)stream);
+    return launch<RLT, 256>(a, a.n_tiles, (hipStream_t)stream);
+  }
   a.n_ct = (E + BC - 1) / BC;
   a.n_rt = (int)((T + 255) / 256);
   const int64_t n_tiles = (int64_t)a.n_rt * a.n_ct;

@@ -170,6 +170,9 @@ def test_sigmoid_router_backward_parity():
     (2048, 1024, 16),     # XS expert count
     (1001, 128, 8),       # ragged T, one column tile mostly empty
     (256, 64, 264),       # E just past one 256-column tile
+    (3000, 512, 200),     # transposed form, 256-expert row tile, ragged T
+    (700, 256, 256),      # transposed form, full 256-expert row tile
+    (77, 1024, 64),       # transposed form, fewer tokens than one column tile
 ])
 def test_router_linear_parity(T, H, E):
     """The MFMA gating linear against fp32 torch on the same bf16 inputs: the
