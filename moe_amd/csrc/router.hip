@@ -109,6 +109,99 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void softmax_topk_kernel(
   }
 }
 
+// DeepSeek router (flat top-k, no expert groups) with G lanes per token, as
+// softmax_topk_group_kernel: scores = sigmoid(logits) stored, selection by
+// rank keys of the biased scores, the winner's unbiased score taken from its
+// owner lane (group max over the one lane that holds it), weights
+// renormalised by their sum in rank order (+1e-20), scaled, cast.  VEC: E ==
+// G*V, fp32 rows moved as 16-byte vectors.
+template <int G, int V, bool VEC>
+__global__ __launch_bounds__(64 * kWavesPerBlock) void sigmoid_topk_group_kernel(
+    const float* __restrict__ logits, const float* __restrict__ bias, int64_t T, int E, int K,
+    int renorm, float scaling, float* __restrict__ scores, void* __restrict__ topk_w,
+    int w_dtype, int64_t* __restrict__ topk_idx, float* __restrict__ tpe) {
+  extern __shared__ int hist[];  // [E] when tpe != nullptr
+  constexpr int TPW = 64 / G;
+  const int lane = threadIdx.x & 63, g = lane & (G - 1), sub = lane / G;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (tpe) {
+    for (int e = threadIdx.x; e < E; e += blockDim.x) hist[e] = 0;
+    __syncthreads();
+  }
+  const int e0 = g * V;
+  const int64_t stride = (int64_t)gridDim.x * kWavesPerBlock * TPW;
+  for (int64_t tb = ((int64_t)blockIdx.x * kWavesPerBlock + wid) * TPW; tb < T; tb += stride) {
+    const int64_t t = tb + sub;
+    const bool tok = t < T;
+    const int64_t tt = tok ? t : T - 1;
+    float sc[V];
+    if constexpr (VEC) {
+      const f32x4* src = (const f32x4*)(logits + tt * E + e0);
+#pragma unroll
+      for (int q = 0; q < V / 4; ++q) {
+        const f32x4 a = src[q];
+#pragma unroll
+        for (int h = 0; h < 4; ++h) sc[4 * q + h] = sigmoidf_(a[h]);
+      }
+      if (tok) {
+        f32x4* dst = (f32x4*)(scores + t * E + e0);
+#pragma unroll
+        for (int q = 0; q < V / 4; ++q)
+          dst[q] = f32x4{sc[4 * q], sc[4 * q + 1], sc[4 * q + 2], sc[4 * q + 3]};
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        const int e = e0 + j;
+        sc[j] = e < E ? sigmoidf_(logits[tt * E + e]) : 0.f;
+        if (tok && e < E) scores[t * E + e] = sc[j];
+      }
+    }
+    uint64_t key[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      const int e = e0 + j;
+      key[j] = e < E ? rank_key(sc[j] + (bias ? bias[e] : 0.0f), e) : 0ull;
+    }
+    float my_w = 0.f, ssum = 0.f;
+    int my_e = 0;
+    for (int k = 0; k < K; ++k) {
+      uint64_t b = key[0];
+#pragma unroll
+      for (int j = 1; j < V; ++j) b = key[j] > b ? key[j] : b;
+      b = group_max_key<G>(b);
+      float own = -INFINITY;  // the winner's unbiased score, on its owner lane
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        const bool hit = key[j] == b;
+        own = hit ? sc[j] : own;
+        key[j] = hit ? 0ull : key[j];
+      }
+      const float sk = group_max<G>(own);
+      ssum += sk;
+      if (g == k) {
+        my_w = sk;
+        my_e = key_index(b);
+      }
+    }
+    if (renorm) my_w = my_w / (ssum + 1e-20f);
+    if (scaling > 0.f) my_w = my_w * scaling;
+    if (tok && g < K) {
+      if (w_dtype == MOE_DTYPE_BF16)
+        ((bf16*)topk_w)[t * K + g] = f2bf(my_w);
+      else
+        ((float*)topk_w)[t * K + g] = my_w;
+      topk_idx[t * K + g] = my_e;
+      if (tpe) atomicAdd(&hist[my_e], 1);
+    }
+  }
+  if (tpe) {
+    __syncthreads();
+    for (int e = threadIdx.x; e < E; e += blockDim.x)
+      if (hist[e]) atomicAdd(&tpe[e], (float)hist[e]);
+  }
+}
+
 // The same softmax router for E <= 16*G experts and K <= G: G lanes per
 // token (64/G tokens per wave), V consecutive experts per lane, ranks through
 // rank_key with G-lane DPP butterflies.  Per token this takes about a fifth
@@ -501,6 +594,71 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void softmax_topk_bwd_kernel(
   }
 }
 
+// The DeepSeek router's backward with G lanes per token (E == G*V, V a
+// multiple of 4, K <= G): rows as 16-byte vectors, the routed (expert,
+// gradient) pairs broadcast from the group's lanes k < K in rank order.
+template <int G, int V>
+__global__ __launch_bounds__(64 * kWavesPerBlock) void sigmoid_topk_bwd_group_kernel(
+    const float* __restrict__ scores, const int64_t* __restrict__ idx,
+    const void* __restrict__ dw, int w_dtype, const float* __restrict__ dscores, int64_t T,
+    int E, int K, int renorm, float scaling, float* __restrict__ dlogits) {
+  static_assert(V % 4 == 0, "16-byte vectors");
+  constexpr int TPW = 64 / G;
+  const int lane = threadIdx.x & 63, g = lane & (G - 1), base = lane - g, sub = lane / G;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int e0 = g * V;
+  const int64_t stride = (int64_t)gridDim.x * kWavesPerBlock * TPW;
+  for (int64_t tb = ((int64_t)blockIdx.x * kWavesPerBlock + wid) * TPW; tb < T; tb += stride) {
+    const int64_t t = tb + sub;
+    const bool tok = t < T;
+    const int64_t tt = tok ? t : T - 1;
+    const int ek = g < K ? (int)idx[tt * K + g] : 0;
+    const float vk = g < K ? scores[tt * E + ek] : 0.f;
+    float gk = 0.f;
+    if (g < K)
+      gk = w_dtype == MOE_DTYPE_BF16 ? bf2f(((const bf16*)dw)[tt * K + g])
+                                     : ((const float*)dw)[tt * K + g];
+    if (scaling > 0.f) gk *= scaling;
+    float dv = gk;
+    if (renorm) {
+      float ssum = 0.f, gv = 0.f;
+      for (int k = 0; k < K; ++k) {
+        ssum += __shfl(vk, base + k, 64);
+        gv += __shfl(gk * vk, base + k, 64);
+      }
+      const float den = ssum + 1e-20f;
+      dv = gk / den - gv / (den * den);
+    }
+    float y[V], ds[V];
+    const f32x4* yrow = (const f32x4*)(scores + tt * E + e0);
+#pragma unroll
+    for (int q = 0; q < V / 4; ++q) {
+      const f32x4 a = yrow[q];
+      const f32x4 d = dscores ? ((const f32x4*)(dscores + tt * E + e0))[q] : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        y[4 * q + h] = a[h];
+        ds[4 * q + h] = d[h];
+      }
+    }
+    for (int k = 0; k < K; ++k) {
+      const int e = __shfl(ek, base + k, 64);
+      const float gg = __shfl(dv, base + k, 64);
+#pragma unroll
+      for (int j = 0; j < V; ++j)
+        if (e == e0 + j) ds[j] += gg;
+    }
+    if (!tok) continue;
+    f32x4* out = (f32x4*)(dlogits + t * E + e0);
+#pragma unroll
+    for (int q = 0; q < V / 4; ++q)
+      out[q] = f32x4{ds[4 * q] * (1.f - y[4 * q]) * y[4 * q],
+                     ds[4 * q + 1] * (1.f - y[4 * q + 1]) * y[4 * q + 1],
+                     ds[4 * q + 2] * (1.f - y[4 * q + 2]) * y[4 * q + 2],
+                     ds[4 * q + 3] * (1.f - y[4 * q + 3]) * y[4 * q + 3]};
+  }
+}
+
 template <int NV>
 __global__ __launch_bounds__(64 * kWavesPerBlock) void sigmoid_topk_bwd_kernel(
     const float* __restrict__ scores, const int64_t* __restrict__ idx,
@@ -686,6 +844,30 @@ extern "C" int moe_amd_router_sigmoid_topk(const float* logits, const float* exp
   if (T == 0) return MOE_OK;
   if (!(scaling_factor > 0.f)) scaling_factor = 0.f;
   size_t shm = tokens_per_expert ? (size_t)E * sizeof(int) : 0;
+  int G, V;
+  group_shape(E, K, G, V);
+  if (num_groups <= 0 && G) {
+    hipStream_t st = (hipStream_t)stream;
+    const bool vec = E == G * V && al16(logits) && al16(scores);
+#define MOE_SIGMOID_GROUP(G_, V_, VEC_)                                                       \
+  sigmoid_topk_group_kernel<G_, V_, VEC_><<<grid_group(T, G_), 64 * kWavesPerBlock, shm, st>>>( \
+      logits, expert_bias, T, E, K, renormalize, scaling_factor, scores, topk_weights,        \
+      weights_dtype, topk_index, tokens_per_expert)
+#define MOE_SIGMOID_GROUP_V(G_, V_)            \
+  do {                                          \
+    if (vec) MOE_SIGMOID_GROUP(G_, V_, true);   \
+    else MOE_SIGMOID_GROUP(G_, V_, false);      \
+  } while (0)
+    if (G == 8 && V == 4) MOE_SIGMOID_GROUP_V(8, 4);
+    else if (G == 8 && V == 8) MOE_SIGMOID_GROUP_V(8, 8);
+    else if (G == 8) MOE_SIGMOID_GROUP_V(8, 16);
+    else if (V == 4) MOE_SIGMOID_GROUP_V(16, 4);
+    else if (V == 8) MOE_SIGMOID_GROUP_V(16, 8);
+    else MOE_SIGMOID_GROUP_V(16, 16);
+#undef MOE_SIGMOID_GROUP_V
+#undef MOE_SIGMOID_GROUP
+    return check_launch("router_sigmoid_topk");
+  }
   if (num_groups > 0) {
     MOE_DISPATCH_NV_G(E, true, sigmoid_topk_kernel, grid_fwd(T), 64 * kWavesPerBlock, shm,
                       (hipStream_t)stream >>>(logits, expert_bias, T, E, K, renormalize,
@@ -717,6 +899,23 @@ extern "C" int moe_amd_router_sigmoid_topk_backward(const float* scores,
               "router_sigmoid_topk_backward: null pointer");
   if (T == 0) return MOE_OK;
   if (!(scaling_factor > 0.f)) scaling_factor = 0.f;
+  int G, V;
+  group_shape(E, K, G, V);
+  if (G && E == G * V && V % 4 == 0 && al16(scores) && al16(d_scores) && al16(d_logits)) {
+    hipStream_t st = (hipStream_t)stream;
+#define MOE_SIGMOID_BWD_GROUP(G_, V_)                                                           \
+  sigmoid_topk_bwd_group_kernel<G_, V_><<<grid_group(T, G_), 64 * kWavesPerBlock, 0, st>>>(     \
+      scores, topk_index, d_topk_weights, weights_dtype, d_scores, T, E, K, renormalize,        \
+      scaling_factor, d_logits)
+    if (G == 8 && V == 4) MOE_SIGMOID_BWD_GROUP(8, 4);
+    else if (G == 8 && V == 8) MOE_SIGMOID_BWD_GROUP(8, 8);
+    else if (G == 8) MOE_SIGMOID_BWD_GROUP(8, 16);
+    else if (V == 4) MOE_SIGMOID_BWD_GROUP(16, 4);
+    else if (V == 8) MOE_SIGMOID_BWD_GROUP(16, 8);
+    else MOE_SIGMOID_BWD_GROUP(16, 16);
+#undef MOE_SIGMOID_BWD_GROUP
+    return check_launch("router_sigmoid_topk_backward");
+  }
   MOE_DISPATCH_NV(E, sigmoid_topk_bwd_kernel, grid_for(T), 64 * kWavesPerBlock, 0,
                   (hipStream_t)stream >>>(scores, topk_index, d_topk_weights, weights_dtype,
                                           d_scores, T, E, K, renormalize, scaling_factor,

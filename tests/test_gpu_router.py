@@ -82,6 +82,9 @@ def test_torch_topk_tie_order_probe():
     (2048, 2048, 1792, 8, None, None, None, torch.bfloat16),   # retrofit router
     (1024, 256, 128, 8, 8, 4, 2.5, torch.float32),             # DeepSeek grouped YAMLs
     (513, 128, 64, 6, None, None, 2.5, torch.float32),
+    (2000, 512, 128, 8, None, None, None, torch.bfloat16),   # DeepSeek YAMLs' E, flat top-k
+    (999, 256, 100, 4, None, None, None, torch.float32),      # lanes partly empty
+    (600, 256, 256, 12, None, None, 1.5, torch.bfloat16),     # 16 lanes per token
 ])
 def test_sigmoid_router_parity(T, H, E, K, groups, gtk, sf, wdt):
     print(f"sigmoid router T={T} E={E} K={K} groups={groups}", flush=True)
@@ -120,8 +123,9 @@ def test_sigmoid_router_parity(T, H, E, K, groups, gtk, sf, wdt):
     assert torch.equal(tpe.cpu(), counts)
     if groups is not None:
         assert all(len(set((r // (E // groups)).tolist())) <= gtk for r in idx.cpu())
-    if sf:
-        assert torch.allclose(w.float().sum(-1).cpu(), torch.full((T,), float(sf)), atol=1e-4)
+    if sf:  # bf16 weights: K roundings of up to half an ulp each
+        assert torch.allclose(w.float().sum(-1).cpu(), torch.full((T,), float(sf)),
+                              atol=1e-4 if wdt == torch.float32 else K * float(sf) * 2.0 ** -9)
 
 
 def test_sigmoid_router_no_nan_at_zero_scores():
@@ -151,16 +155,20 @@ def test_softmax_router_backward_parity(renorm, E, K, with_dp):
     assert _rel(gl.float(), ref) < 1e-2  # bf16 output rounding
 
 
-def test_sigmoid_router_backward_parity():
-    g = torch.Generator().manual_seed(22)
-    T, E, K = 1024, 256, 8
+@pytest.mark.parametrize("E,K,wdt", [(256, 8, torch.float32), (128, 8, torch.bfloat16),
+                                     (100, 4, torch.float32), (1792, 8, torch.bfloat16)])
+def test_sigmoid_router_backward_parity(E, K, wdt):
+    print(f"sigmoid router backward E={E} K={K} {wdt}", flush=True)
+    g = torch.Generator().manual_seed(22 + E)
+    T = 1024 + 5
     logits = torch.randn(T, E, generator=g).to(DEV).requires_grad_(True)
     bias = (torch.rand(E, generator=g) - 0.5).to(DEV)
-    scores, w, idx = sigmoid_topk(logits, bias, K, True, 2.5, None, None, torch.float32, None)
+    scores, w, idx = sigmoid_topk(logits, bias, K, True, 2.5, None, None, wdt, None)
     dw = torch.randn(T, K, generator=g).to(DEV)
     ds = torch.randn(T, E, generator=g).to(DEV) * 0.1
-    (gl,) = torch.autograd.grad((w * dw).sum() + (scores * ds).sum(), logits)
-    ref = O.sigmoid_router_backward(scores.detach().cpu(), idx.cpu(), dw.cpu(), ds.cpu(), True, 2.5)
+    (gl,) = torch.autograd.grad((w.float() * dw).sum() + (scores * ds).sum(), logits)
+    ref = O.sigmoid_router_backward(scores.detach().cpu(), idx.cpu(), dw.to(wdt).float().cpu(),
+                                    ds.cpu(), True, 2.5)
     assert torch.allclose(gl.cpu(), ref, rtol=1e-5, atol=1e-6)
 
 
