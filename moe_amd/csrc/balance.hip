@@ -296,6 +296,106 @@ __global__ __launch_bounds__(64) void topk_stats_finalize_kernel(
 // s' = s / (sum s + 1e-20) per token; per block the selection counts of the
 // sequence's experts (the routed indices if given, else the top-k of s') and
 // the sums of s'.
+// seq_stats with G lanes per token (as topk_stats_group_kernel): block
+// (chunk c, sequence b) covers kSeqChunk tokens; the partial is the sum over
+// the block's token groups in group order through LDS.
+template <int G, int V>
+__global__ __launch_bounds__(64 * kWaves) void seq_stats_group_kernel(
+    const void* __restrict__ scores, int dtype, const int64_t* __restrict__ selected, int64_t S,
+    int E, int K, float* __restrict__ part_cnt, float* __restrict__ part_sum) {
+  constexpr int TPW = 64 / G, ROWS = kWaves * TPW;
+  extern __shared__ float sbuf[];  // [ROWS][E]
+  const int lane = threadIdx.x & 63, g = lane & (G - 1), sub = lane / G;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int row = wid * TPW + sub, e0 = g * V;
+  const int b = blockIdx.y, c = blockIdx.x;
+  const bool vec = E == G * V && (dtype == MOE_DTYPE_F32 ? V % 4 == 0 : V % 8 == 0) &&
+                   (((uintptr_t)scores & 15) == 0);
+  float cnt[V], psum[V];
+#pragma unroll
+  for (int j = 0; j < V; ++j) cnt[j] = psum[j] = 0.f;
+  const int64_t s0 = (int64_t)c * kSeqChunk;
+  const int64_t s1 = s0 + kSeqChunk < S ? s0 + kSeqChunk : S;
+  for (int64_t sb = s0 + (int64_t)wid * TPW; sb < s1; sb += kWaves * TPW) {
+    const int64_t st = sb + sub;
+    const bool tok = st < s1;
+    const int64_t t = (int64_t)b * S + (tok ? st : s1 - 1);
+    float v[V];
+    if (vec) {
+      if (dtype == MOE_DTYPE_F32) {
+        const f32x4* src = (const f32x4*)((const float*)scores + t * E + e0);
+#pragma unroll
+        for (int q = 0; q < V / 4; ++q) {
+          const f32x4 a = src[q];
+#pragma unroll
+          for (int h = 0; h < 4; ++h) v[4 * q + h] = a[h];
+        }
+      } else {
+        const u32x4* src = (const u32x4*)((const bf16*)scores + t * E + e0);
+#pragma unroll
+        for (int q = 0; q < (V + 7) / 8; ++q) {
+          const u32x4 a = src[q];
+#pragma unroll
+          for (int h = 0; h < 8; ++h)
+            if (8 * q + h < V) v[8 * q + h] = (h & 1) ? bf_hi(a[h >> 1]) : bf_lo(a[h >> 1]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < V; ++j) v[j] = e0 + j < E ? load_val(scores, dtype, t * E + e0 + j) : 0.f;
+    }
+    float rs = 0.f;
+#pragma unroll
+    for (int j = 0; j < V; ++j) rs += v[j];
+    rs = group_sum<G>(rs) + 1e-20f;
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      v[j] = v[j] / rs;
+      if (tok && e0 + j < E) psum[j] += v[j];
+    }
+    if (selected) {
+      for (int k = 0; k < K; ++k) {
+        const int64_t ek = selected[t * K + k];
+#pragma unroll
+        for (int j = 0; j < V; ++j)
+          if (tok && ek == e0 + j) cnt[j] += 1.f;
+      }
+    } else {
+      uint64_t key[V];
+#pragma unroll
+      for (int j = 0; j < V; ++j) key[j] = e0 + j < E ? rank_key(v[j], e0 + j) : 0ull;
+      for (int k = 0; k < K; ++k) {
+        uint64_t m = key[0];
+#pragma unroll
+        for (int j = 1; j < V; ++j) m = key[j] > m ? key[j] : m;
+        m = group_max_key<G>(m);
+#pragma unroll
+        for (int j = 0; j < V; ++j) key[j] = key[j] == m ? 0ull : key[j];
+      }
+      if (tok) {
+#pragma unroll
+        for (int j = 0; j < V; ++j)
+          if (e0 + j < E && key[j] == 0ull) cnt[j] += 1.f;  // selected (real keys are never 0)
+      }
+    }
+  }
+  const size_t slot = ((size_t)b * gridDim.x + c) * E;
+  auto combine = [&](const float (&acc)[V], float* out) {
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < V; ++j)
+      if (e0 + j < E) sbuf[row * E + e0 + j] = acc[j];
+    __syncthreads();
+    for (int e = threadIdx.x; e < E; e += blockDim.x) {
+      float sm = 0.f;
+      for (int r = 0; r < ROWS; ++r) sm += sbuf[r * E + e];
+      out[e] = sm;
+    }
+  };
+  combine(cnt, part_cnt + slot);
+  combine(psum, part_sum + slot);
+}
+
 template <int NV>
 __global__ __launch_bounds__(64 * kWaves) void seq_stats_kernel(
     const void* __restrict__ scores, int dtype, const int64_t* __restrict__ selected, int64_t S,
@@ -632,8 +732,24 @@ extern "C" int moe_amd_seq_stats(const void* scores, int scores_dtype,
   hipStream_t st = (hipStream_t)stream;
   float* pc = (float*)workspace;
   float* ps = pc + (size_t)B * nc * E;
-  MOE_DISPATCH_NV_B(E, seq_stats_kernel, dim3(nc, B), 64 * kWaves, 0, st>>>(
-      scores, scores_dtype, selected, S, E, K, pc, ps));
+  int G, V;
+  group_shape(E, K, G, V);
+  if (G) {
+    const size_t shm = (size_t)kWaves * (64 / G) * E * sizeof(float);
+#define MOE_SEQ_GROUP(G_, V_)                                                                 \
+  seq_stats_group_kernel<G_, V_><<<dim3(nc, B), 64 * kWaves, shm, st>>>(scores, scores_dtype, \
+                                                                        selected, S, E, K, pc, ps)
+    if (G == 8 && V == 4) MOE_SEQ_GROUP(8, 4);
+    else if (G == 8 && V == 8) MOE_SEQ_GROUP(8, 8);
+    else if (G == 8) MOE_SEQ_GROUP(8, 16);
+    else if (V == 4) MOE_SEQ_GROUP(16, 4);
+    else if (V == 8) MOE_SEQ_GROUP(16, 8);
+    else MOE_SEQ_GROUP(16, 16);
+#undef MOE_SEQ_GROUP
+  } else {
+    MOE_DISPATCH_NV_B(E, seq_stats_kernel, dim3(nc, B), 64 * kWaves, 0, st>>>(
+        scores, scores_dtype, selected, S, E, K, pc, ps));
+  }
   seq_stats_finalize_kernel<<<(unsigned)((int64_t)B * E), 64, 0, st>>>(pc, ps, nc, B, E, S,
                                                                         counts, mean_scores);
   return check_launch(who);
