@@ -223,7 +223,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
   constexpr int TI = 4;                                   // MFMA col sub-tiles per wave (128 cols)
   constexpr int CPW = BC * BK * 2 / 1024 / NW;            // 1 KB DMA blocks per wave, column half
   constexpr int RPW = BR * BK * 2 / 1024 / NW;            // ... row half
-  constexpr int NTOK = GCOL ? CPW : 0;                    // gathered-row indices per lane and stage
+  constexpr int NTOK = GCOL ? 1 : 0;                      // gathered-row index loads per stage
   constexpr int NOPS = NTOK + RPW + CPW;                  // memory ops per main-loop step
   constexpr int NGRP = (BK / 16) * TI;                    // MFMA groups per step
   static_assert(CPW * NW == 32 && RPW * NW * 8 == BR && TJ >= 1, "DMA blocks per wave");
@@ -474,17 +474,13 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       if (tid < BR) erow_src = p.row_src[min(d.row0 + tid, d.row_end - 1)];
   };
 
-  // G1DW, G2DWG: raw row_src entries of stage s (one per column block of
-  // this lane).  Reads past S return zero; rows past the expert's range are
-  // masked when the DMA offsets are formed.
+  // G1DW, G2DWG: raw row_src entries of stage s, one 64-lane load per wave
+  // (lane L: k row L of the stage); a column block's two k rows are read
+  // out of it with v_readlane when its DMA offsets are formed.  Reads past S
+  // return zero; rows past the expert's range are masked there.
   auto fetch_tok = [&](int s, int (&tk)[NTOK > 0 ? NTOK : 1]) {
-    if constexpr (GCOL) {
-#pragma unroll
-      for (int i = 0; i < NTOK; ++i) {
-        const int kr = s * BK + km_krow(wid + NW * i);
-        tk[i] = __builtin_amdgcn_raw_buffer_load_b32(isrc, (uint32_t)(kb_cur + kr) * 4, 0, 0);
-      }
-    }
+    if constexpr (GCOL)
+      tk[0] = __builtin_amdgcn_raw_buffer_load_b32(isrc, (uint32_t)(kb_cur + s * BK + lane) * 4, 0, 0);
   };
 
   auto slot_ptr = [&](int h) { return (char*)smem + (h % NSLOT) * SLOT; };
@@ -492,9 +488,13 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
   // DMA of the column half of stage s (ring position 2s).
   auto col_off = [&](int s, int i, const int (&tk)[NTOK > 0 ? NTOK : 1]) -> uint32_t {
     if constexpr (GCOL) {
-      const int kr = s * BK + km_krow(wid + NW * i);
+      const int blk = wid + NW * i;  // wave-uniform: k rows 2*blk and 2*blk+1
+      const int kr = s * BK + km_krow(blk);
+      const int ta = __builtin_amdgcn_readlane(tk[0], 2 * blk);
+      const int tb = __builtin_amdgcn_readlane(tk[0], 2 * blk + 1);
+      const int src = (lane >> 5) ? tb : ta;
       // Branch-free select (rows past the expert's range read zeros).
-      const uint32_t v = (uint32_t)div_topk(tk[i], p.tok_mul, p.tok_shift) * (uint32_t)(H * 2) + coff[i];
+      const uint32_t v = (uint32_t)div_topk(src, p.tok_mul, p.tok_shift) * (uint32_t)(H * 2) + coff[i];
       const uint32_t m = 0u - (uint32_t)(kr < ke_cur - kb_cur);
       return (v & m) | (kOOB & ~m);
     } else {
@@ -630,10 +630,9 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       // Op o of window W(w); `tk` holds the row_src entries of stage w+2.
       auto win_op = [&](int w, int o, const int (&tk)[NTOK > 0 ? NTOK : 1]) {
         if (o < NTOK) {
-          if constexpr (GCOL) {
-            const int kr = (w + 3) * BK + km_krow(wid + NW * o);
-            tn[o] = __builtin_amdgcn_raw_buffer_load_b32(isrc, (uint32_t)(kb_cur + kr) * 4, 0, 0);
-          }
+          if constexpr (GCOL)
+            tn[0] = __builtin_amdgcn_raw_buffer_load_b32(
+                isrc, (uint32_t)(kb_cur + (w + 3) * BK + lane) * 4, 0, 0);
         } else if (o < NTOK + RPW) {
           const int i = o - NTOK;
           const auto rs = stage_rsrc(rptr, rbytes, (uint32_t)(w + 1) * rstep);
