@@ -56,6 +56,8 @@
 //
 // Reference: transformers/integrations/moe.py:439-459 (forward grouped_mm),
 // :226-242 (per-expert dX / dW formulas of the backward).
+#include <atomic>
+
 #include "common.h"
 
 namespace moe {
@@ -986,18 +988,20 @@ void set_topk(GemmArgs& a, int top_k) {
   a.tok_mul = (uint32_t)((((uint64_t)1 << (31 + sh)) + (uint64_t)top_k - 1) / (uint64_t)top_k);
 }
 
-int g_num_cu[64];
+// Per-device CU count, filled on first use; atomics because host threads
+// may launch on the same device concurrently (they store the same value).
+std::atomic<int> g_num_cu[64];
 
 int num_cus() {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!g_num_cu[dev]) {
-    int n = 0;
+  int n = g_num_cu[dev].load(std::memory_order_relaxed);
+  if (!n) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
       n = 256;
-    g_num_cu[dev] = n;
+    g_num_cu[dev].store(n, std::memory_order_relaxed);
   }
-  return g_num_cu[dev];
+  return n;
 }
 
 template <int MODE, int BR>
