@@ -78,11 +78,30 @@ int moe_amd_router_linear_backward_dx(const void* d_logits, const void* weight, 
  * F.linear's backward.  Split over token chunks (one fp32 partial per chunk
  * in the caller's workspace, moe_amd_router_linear_backward_dw_workspace_size
  * bytes), reduced in chunk order: deterministic.  H multiple of 256; E a
- * multiple of 8, at most 256. */
+ * multiple of 8. */
 size_t moe_amd_router_linear_backward_dw_workspace_size(int64_t T, int E, int H);
 int moe_amd_router_linear_backward_dw(const void* d_logits, const void* hidden_states, int64_t T,
                                       int E, int H, void* workspace, size_t workspace_bytes,
                                       void* d_weight, void* stream);
+
+/* Both gradients of the gating linear for fp32 logits: the DeepSeek router's
+ * F.linear(h.float(), W.float()) (src/models/router.py:107-109), whose
+ * autograd computes d_x = bf16(d_logits . W) and d_weight =
+ * bf16(d_logits^T . h) in fp32 arithmetic (replaces those two fp32 GEMMs).
+ * Each fp32 d_logits element g is split into two bf16 terms, hi = bf16(g)
+ * and lo = bf16(g - hi), |g - hi - lo| <= 2^-18 |g|; both gradients then run
+ * on the bf16 MFMA kernels (exact products, fp32 sums) with the two terms
+ * stacked along the reduction: d_x = [hi|lo] . [W;W], d_weight = the hi and
+ * lo partial products added in fp32 before the one bf16 rounding.  d_x or
+ * d_weight may be NULL (that gradient is skipped).  d_logits [T,E] fp32;
+ * hidden_states [T,H], weight [E,H], d_x, d_weight bf16.  H multiple of 256,
+ * E of 32.  Workspace: moe_amd_router_linear_backward_f32_workspace_size
+ * bytes. */
+size_t moe_amd_router_linear_backward_f32_workspace_size(int64_t T, int E, int H);
+int moe_amd_router_linear_backward_f32(const float* d_logits, const void* hidden_states,
+                                       const void* weight, int64_t T, int E, int H,
+                                       void* workspace, size_t workspace_bytes, void* d_x,
+                                       void* d_weight, void* stream);
 
 /* Softmax router after the gating linear: probs = softmax(float(logits) +
  * logit_offset) over E, top-K (value descending, lower expert id first on

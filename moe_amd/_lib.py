@@ -40,6 +40,8 @@ SIGNATURES: dict[str, tuple] = {
     "moe_amd_router_linear_backward_dx": (_i, [_p, _p, _i64, _i, _i, _p, _p]),
     "moe_amd_router_linear_backward_dw_workspace_size": (_sz, [_i64, _i, _i]),
     "moe_amd_router_linear_backward_dw": (_i, [_p, _p, _i64, _i, _i, _p, _sz, _p, _p]),
+    "moe_amd_router_linear_backward_f32_workspace_size": (_sz, [_i64, _i, _i]),
+    "moe_amd_router_linear_backward_f32": (_i, [_p, _p, _p, _i64, _i, _i, _p, _sz, _p, _p, _p]),
     "moe_amd_router_softmax_topk": (_i, [_p, _i, _p, _i64, _i, _i, _i, _p, _p, _p, _p, _p]),
     "moe_amd_router_softmax_topk_backward": (_i, [_p, _p, _p, _p, _i64, _i, _i, _i, _p, _i, _p]),
     "moe_amd_router_sigmoid_topk": (

@@ -1175,6 +1175,30 @@ extern "C" int moe_amd_router_linear(const void* hidden_states, const void* weig
   return launch<RL, 256>(a, a.n_tiles, (hipStream_t)stream);
 }
 
+namespace {
+
+// d_x[T][H] = bf16(a[T][K] . w[K][H]) on RDX (the reduction runs over the K
+// rows of w).  Shapes checked by the callers.
+int rdx_run(const void* a_rows, const void* w, int64_t T, int K, int H, void* d_x,
+            hipStream_t st, const char* who) {
+  MOE_REQUIRE((int64_t)K * H * 2 < ((int64_t)1 << 31), MOE_ERR_UNSUPPORTED,
+              "%s: router weight too large", who);
+  if (T == 0) return MOE_OK;
+  GemmArgs a{};
+  a.w = (const bf16*)w;
+  a.a0 = (const bf16*)a_rows;
+  a.out = (bf16*)d_x;
+  a.T = T; a.E = K; a.H = H; a.I = 64;
+  a.n_ct = H / BC;
+  a.n_rt = (int)((T + 255) / 256);
+  const int64_t n_tiles = (int64_t)a.n_rt * a.n_ct;
+  MOE_REQUIRE(n_tiles < ((int64_t)1 << 30), MOE_ERR_UNSUPPORTED, "%s: too many tiles", who);
+  a.n_tiles = (int)n_tiles;
+  return launch<RDX, 256>(a, a.n_tiles, st);
+}
+
+}  // namespace
+
 extern "C" int moe_amd_router_linear_backward_dx(const void* d_logits, const void* weight,
                                                  int64_t T, int E, int H, void* d_x,
                                                  void* stream) {
@@ -1186,47 +1210,119 @@ extern "C" int moe_amd_router_linear_backward_dx(const void* d_logits, const voi
   MOE_ALIGNED(d_logits, who);
   MOE_ALIGNED(weight, who);
   MOE_ALIGNED(d_x, who);
-  MOE_REQUIRE((int64_t)E * H * 2 < ((int64_t)1 << 31), MOE_ERR_UNSUPPORTED,
-              "%s: router weight too large", who);
-  if (T == 0) return MOE_OK;
-  GemmArgs a{};
-  a.w = (const bf16*)weight;
-  a.a0 = (const bf16*)d_logits;
-  a.out = (bf16*)d_x;
-  a.T = T; a.E = E; a.H = H; a.I = 64;
-  a.n_ct = H / BC;
-  a.n_rt = (int)((T + 255) / 256);
-  const int64_t n_tiles = (int64_t)a.n_rt * a.n_ct;
-  MOE_REQUIRE(n_tiles < ((int64_t)1 << 30), MOE_ERR_UNSUPPORTED, "%s: too many tiles", who);
-  a.n_tiles = (int)n_tiles;
-  return launch<RDX, 256>(a, a.n_tiles, (hipStream_t)stream);
+  return rdx_run(d_logits, weight, T, E, H, d_x, (hipStream_t)stream, who);
 }
+
+namespace {
 
 // Split-K reduction of RDW: d_w[e][h] = bf16(sum_c partial[c][e][h]), fp32
 // sums in chunk order (deterministic); 4 elements per thread (n % 4 == 0).
-// With no chunks it writes zeros.
+// With halves = 2 each chunk's partial holds 2n values, [hi rows | lo rows]
+// of a two-term split (see moe_amd_router_linear_backward_f32), and both
+// halves are added, hi then lo, chunk by chunk.  With no chunks it writes
+// zeros.
 __global__ void reduce_chunks_kernel(const float* __restrict__ part, int nchunk, int64_t n,
-                                     bf16* __restrict__ out) {
+                                     int halves, bf16* __restrict__ out) {
   const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
   if (i >= n) return;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int c = 0; c < nchunk; ++c) acc += *(const f32x4*)(part + (int64_t)c * n + i);
+  for (int c = 0; c < nchunk; ++c)
+    for (int h = 0; h < halves; ++h)
+      acc += *(const f32x4*)(part + ((int64_t)c * halves + h) * n + i);
   u32x2 w = {pack_bf2(acc[0], acc[1]), pack_bf2(acc[2], acc[3])};
   *(u32x2*)(out + i) = w;
 }
 
-int rdw_chunks(int64_t T, int H) {
-  // about one workgroup per CU: chunks x (H / 256) column tiles
-  int c = num_cus() / (H / BC);
+int rdw_chunks(int64_t T, int H, int E) {
+  // about one workgroup per CU: chunks x (E / 256) row tiles x (H / 256) column tiles
+  const int per_chunk = (H / BC) * ((E + 255) / 256);
+  int c = num_cus() / (per_chunk > 0 ? per_chunk : 1);
   if (c < 1) c = 1;
   const int64_t max_c = (T + 63) / 64;  // at least 64 tokens per chunk
   if (c > max_c) c = (int)max_c;
   return c < 1 ? 1 : c;
 }
 
-extern "C" size_t moe_amd_router_linear_backward_dw_workspace_size(int64_t T, int E, int H) {
+size_t rdw_workspace(int64_t T, int E, int H) {
   if (T <= 0 || E <= 0 || H < BC) return 0;
-  return (size_t)rdw_chunks(T, H) * (size_t)E * (size_t)H * sizeof(float);
+  return (size_t)rdw_chunks(T, H, E) * (size_t)E * (size_t)H * sizeof(float);
+}
+
+// d_w[E/halves][H] = bf16(g[T][E]^T . x[T][H]) (rows of the two halves
+// summed when halves = 2) on RDW, split over token chunks into fp32 partials
+// in ws, then reduced.  Shapes and workspace checked by the callers.
+int rdw_run(const void* g, const void* x, int64_t T, int E, int H, void* ws, int halves,
+            void* d_w, hipStream_t st, const char* who) {
+  const int64_t n = (int64_t)(E / halves) * H;
+  if (T == 0) {  // no tokens: a zero gradient (a fill kernel, safe under graph capture)
+    reduce_chunks_kernel<<<(unsigned)((n / 4 + 255) / 256), 256, 0, st>>>(nullptr, 0, n, 1,
+                                                                         (bf16*)d_w);
+    return check_launch(who);
+  }
+  const int nchunk = rdw_chunks(T, H, E);
+  const int64_t chunk_rows = (T + nchunk - 1) / nchunk;
+  // chunk byte extents and the d_logits/x offsets stay below 2^31
+  MOE_REQUIRE(chunk_rows * (int64_t)(H > E ? H : E) * 2 < ((int64_t)1 << 31),
+              MOE_ERR_UNSUPPORTED, "%s: token chunk too large", who);
+  GemmArgs a{};
+  a.a0 = (const bf16*)g;
+  a.x = (const bf16*)x;
+  a.out_f32 = (float*)ws;
+  a.T = T; a.E = E; a.H = H; a.I = 64;
+  a.chunk_rows = (int)chunk_rows;
+  a.n_rt = (E + 255) / 256;
+  a.n_ct = H / BC;
+  const int64_t n_tiles = (int64_t)nchunk * a.n_rt * a.n_ct;
+  MOE_REQUIRE(n_tiles < ((int64_t)1 << 30), MOE_ERR_UNSUPPORTED, "%s: too many tiles", who);
+  a.n_tiles = (int)n_tiles;
+  int rc = launch<RDW, 256>(a, a.n_tiles, st);
+  if (rc) return rc;
+  reduce_chunks_kernel<<<(unsigned)((n / 4 + 255) / 256), 256, 0, st>>>(
+      (const float*)ws, nchunk, n, halves, (bf16*)d_w);
+  return check_launch(who);
+}
+
+// Two-term bf16 split of fp32 gradients: row t of out [T][2E] holds
+// hi = bf16(g[t]) in columns 0..E-1 and lo = bf16(g[t] - hi) in E..2E-1
+// (g - hi is exact in fp32, so |g - hi - lo| <= 2^-18 |g|).  4 elements per
+// thread (E % 4 == 0).
+__global__ void split_bf16x2_kernel(const float* __restrict__ g, int64_t T, int E,
+                                    bf16* __restrict__ out) {
+  const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (i >= T * E) return;
+  const int64_t t = i / E;
+  const int e = (int)(i - t * E);
+  const f32x4 v = *(const f32x4*)(g + i);
+  float hi[4], lo[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    hi[q] = round_bf(v[q]);
+    lo[q] = v[q] - hi[q];
+  }
+  bf16* row = out + t * 2 * E + e;
+  *(u32x2*)row = u32x2{pack_bf2(hi[0], hi[1]), pack_bf2(hi[2], hi[3])};
+  *(u32x2*)(row + E) = u32x2{pack_bf2(lo[0], lo[1]), pack_bf2(lo[2], lo[3])};
+}
+
+// Workspace layout of moe_amd_router_linear_backward_f32: the split
+// [T][2E] bf16, the stacked weight [2E][H] bf16, RDW's partials.
+struct F32Ws {
+  size_t split, wdup, part, total;
+};
+F32Ws f32_ws(int64_t T, int E, int H) {
+  F32Ws w{};
+  if (T <= 0 || E <= 0 || H <= 0) return w;
+  w.split = align_up((size_t)T * 2 * E * sizeof(bf16), 256);
+  w.wdup = align_up((size_t)2 * E * H * sizeof(bf16), 256);
+  w.part = align_up(rdw_workspace(T, 2 * E, H), 256);
+  w.total = w.split + w.wdup + w.part;
+  return w;
+}
+
+}  // namespace
+
+extern "C" size_t moe_amd_router_linear_backward_dw_workspace_size(int64_t T, int E, int H) {
+  return rdw_workspace(T, E, H);
 }
 
 extern "C" int moe_amd_router_linear_backward_dw(const void* d_logits, const void* hidden_states,
@@ -1235,43 +1331,72 @@ extern "C" int moe_amd_router_linear_backward_dw(const void* d_logits, const voi
                                                  void* stream) {
   const char* who = "router_linear_backward_dw";
   MOE_REQUIRE(T >= 0 && E >= 1 && H > 0, MOE_ERR_ARG, "%s: bad sizes", who);
-  MOE_REQUIRE(H % 256 == 0 && E % 8 == 0 && E <= 256, MOE_ERR_ARG,
-              "%s: H=%d must be a multiple of 256 and E=%d of 8, at most 256", who, H, E);
+  MOE_REQUIRE(H % 256 == 0 && E % 8 == 0, MOE_ERR_ARG,
+              "%s: H=%d must be a multiple of 256 and E=%d of 8", who, H, E);
   MOE_REQUIRE(d_weight && (T == 0 || (d_logits && hidden_states)), MOE_ERR_ARG,
               "%s: null pointer", who);
   MOE_ALIGNED(d_logits, who);
   MOE_ALIGNED(hidden_states, who);
   MOE_ALIGNED(d_weight, who);
-  hipStream_t st = (hipStream_t)stream;
-  const int64_t n = (int64_t)E * H;
-  if (T == 0) {  // no tokens: a zero gradient (a fill kernel, safe under graph capture)
-    reduce_chunks_kernel<<<(unsigned)((n / 4 + 255) / 256), 256, 0, st>>>(nullptr, 0, n,
-                                                                         (bf16*)d_weight);
-    return check_launch(who);
+  if (T > 0) {
+    const size_t need = rdw_workspace(T, E, H);
+    MOE_REQUIRE(workspace && workspace_bytes >= need, MOE_ERR_WORKSPACE,
+                "%s: workspace of %zu bytes needed", who, need);
+    MOE_ALIGNED(workspace, who);
   }
-  const size_t need = moe_amd_router_linear_backward_dw_workspace_size(T, E, H);
-  MOE_REQUIRE(workspace && workspace_bytes >= need, MOE_ERR_WORKSPACE,
-              "%s: workspace of %zu bytes needed", who, need);
+  return rdw_run(d_logits, hidden_states, T, E, H, workspace, 1, d_weight, (hipStream_t)stream,
+                 who);
+}
+
+extern "C" size_t moe_amd_router_linear_backward_f32_workspace_size(int64_t T, int E, int H) {
+  return f32_ws(T, E, H).total;
+}
+
+extern "C" int moe_amd_router_linear_backward_f32(const float* d_logits, const void* hidden_states,
+                                                  const void* weight, int64_t T, int E, int H,
+                                                  void* workspace, size_t workspace_bytes,
+                                                  void* d_x, void* d_weight, void* stream) {
+  const char* who = "router_linear_backward_f32";
+  MOE_REQUIRE(T >= 0 && E >= 1 && H > 0, MOE_ERR_ARG, "%s: bad sizes", who);
+  MOE_REQUIRE(H % 256 == 0 && E % 32 == 0, MOE_ERR_ARG,
+              "%s: H=%d must be a multiple of 256 and E=%d of 32", who, H, E);
+  MOE_REQUIRE((!d_x || weight) && (T == 0 || (d_logits && (!d_weight || hidden_states))),
+              MOE_ERR_ARG, "%s: null pointer", who);
+  MOE_ALIGNED(d_logits, who);
+  MOE_ALIGNED(hidden_states, who);
+  MOE_ALIGNED(weight, who);
+  MOE_ALIGNED(d_x, who);
+  MOE_ALIGNED(d_weight, who);
+  MOE_REQUIRE((int64_t)2 * E * H * 2 < ((int64_t)1 << 31), MOE_ERR_UNSUPPORTED,
+              "%s: router weight too large", who);
+  hipStream_t st = (hipStream_t)stream;
+  if (T == 0) {
+    if (d_weight) return rdw_run(nullptr, nullptr, 0, E, H, nullptr, 1, d_weight, st, who);
+    return MOE_OK;
+  }
+  const F32Ws L = f32_ws(T, E, H);
+  MOE_REQUIRE(workspace && workspace_bytes >= L.total, MOE_ERR_WORKSPACE,
+              "%s: workspace of %zu bytes needed", who, L.total);
   MOE_ALIGNED(workspace, who);
-  const int nchunk = rdw_chunks(T, H);
-  const int64_t chunk_rows = (T + nchunk - 1) / nchunk;
-  // chunk byte extents and the d_logits/x offsets stay below 2^31
-  MOE_REQUIRE(chunk_rows * (int64_t)H * 2 < ((int64_t)1 << 31), MOE_ERR_UNSUPPORTED,
-              "%s: token chunk too large", who);
-  GemmArgs a{};
-  a.a0 = (const bf16*)d_logits;
-  a.x = (const bf16*)hidden_states;
-  a.out_f32 = (float*)workspace;
-  a.T = T; a.E = E; a.H = H; a.I = 64;
-  a.chunk_rows = (int)chunk_rows;
-  a.n_rt = 1;
-  a.n_ct = H / BC;
-  a.n_tiles = nchunk * a.n_ct;
-  int rc = launch<RDW, 256>(a, a.n_tiles, st);
+  MOE_REQUIRE(T * 2 * E < ((int64_t)1 << 40), MOE_ERR_UNSUPPORTED, "%s: too many tokens", who);
+  char* base = (char*)workspace;
+  bf16* split = (bf16*)base;
+  bf16* wdup = (bf16*)(base + L.split);
+  void* part = base + L.split + L.wdup;
+  const int64_t n4 = T * E / 4;
+  split_bf16x2_kernel<<<(unsigned)((n4 + 255) / 256), 256, 0, st>>>(d_logits, T, E, split);
+  int rc = check_launch(who);
   if (rc) return rc;
-  reduce_chunks_kernel<<<(unsigned)((n / 4 + 255) / 256), 256, 0, st>>>(
-      (const float*)workspace, nchunk, n, (bf16*)d_weight);
-  return check_launch(who);
+  if (d_x) {
+    const size_t wb = (size_t)E * H * sizeof(bf16);
+    if (hipMemcpyAsync(wdup, weight, wb, hipMemcpyDeviceToDevice, st) != hipSuccess ||
+        hipMemcpyAsync((char*)wdup + wb, weight, wb, hipMemcpyDeviceToDevice, st) != hipSuccess)
+      return check_launch(who);
+    rc = rdx_run(split, wdup, T, 2 * E, H, d_x, st, who);
+    if (rc) return rc;
+  }
+  if (d_weight) return rdw_run(split, hidden_states, T, 2 * E, H, part, 2, d_weight, st, who);
+  return MOE_OK;
 }
 
 extern "C" int moe_amd_gemm_down_backward_dx_dswiglu(const void* dy, const int32_t* offsets,

@@ -154,14 +154,19 @@ def _(x, weight, out_dtype):
 def router_linear_backward(d_logits: Tensor, x: Tensor, weight: Tensor, out_dtype: torch.dtype,
                            need_x: bool, need_w: bool) -> tuple[Tensor, Tensor]:
     """(d_x, d_W).  bf16 logits: the MFMA dX and split-K dW kernels (fp32
-    accumulation, one bf16 rounding, as F.linear's bf16 backward) where H is a
-    multiple of 256 (dW: E <= 256), else torch in bf16; fp32 logits: torch in
-    fp32, cast to the inputs' dtypes."""
+    accumulation, one bf16 rounding, as F.linear's bf16 backward); fp32
+    logits (the DeepSeek router's fp32 linear): the same kernels on a
+    two-term bf16 split of d_logits, fp32-accurate, each gradient rounded
+    once to the inputs' bf16.  H a multiple of 256 (and E of 32 for fp32
+    logits), else torch on the same device in the logits' precision."""
     E, H = weight.shape
     dx = x.new_empty(0)
     dw = weight.new_empty(0)
+    bf = x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16
     if out_dtype == torch.float32:
         g = d_logits.float()
+        if bf and H % 256 == 0 and E % 32 == 0:
+            return ops.router_linear_backward_f32(g, x, weight, need_x, need_w)
         if need_x:
             dx = (g @ weight.float()).to(x.dtype)
         if need_w:
@@ -171,7 +176,7 @@ def router_linear_backward(d_logits: Tensor, x: Tensor, weight: Tensor, out_dtyp
         if need_x:
             dx = ops.router_linear_backward_dx(g, weight) if H % 256 == 0 else g @ weight
         if need_w:
-            dw = (ops.router_linear_backward_dw(g, x) if H % 256 == 0 and E <= 256
+            dw = (ops.router_linear_backward_dw(g, x) if H % 256 == 0
                   else g.t().contiguous() @ x)
     return dx, dw
 
@@ -392,10 +397,7 @@ def moe_layer_bwd(d_out: Optional[Tensor], d_probs: Optional[Tensor], d_w: Optio
                                                 torch.bfloat16)
     d_wr = w_router.new_empty(0)
     if need_wr:
-        if w_router.shape[0] <= 256:
-            d_wr = ops.router_linear_backward_dw(d_logits, x)
-        else:
-            d_wr = d_logits.t().contiguous() @ x
+        d_wr = ops.router_linear_backward_dw(d_logits, x)
     d_x = x.new_empty(0)
     if need_x:
         d_xs = ops.gemm_gate_up_backward_dx(d_gu, plan, gate_up_proj)

@@ -104,9 +104,40 @@ def router_linear_backward_dx(d_logits: torch.Tensor, weight: torch.Tensor) -> t
     return d_x
 
 
+def router_linear_backward_f32(d_logits: torch.Tensor, x: torch.Tensor, weight: torch.Tensor,
+                               need_x: bool = True, need_w: bool = True):
+    """(d_x, d_weight) of the fp32 gating linear F.linear(h.float(), W.float())
+    for fp32 d_logits [T,E] and bf16 x [T,H], weight [E,H]: fp32-accurate
+    products from a two-term bf16 split of d_logits on the MFMA kernels, each
+    gradient rounded once to bf16.  A gradient not asked for is an empty
+    tensor."""
+    _need_cuda(d_logits, x, weight)
+    if (d_logits.dtype != torch.float32 or x.dtype != torch.bfloat16
+            or weight.dtype != torch.bfloat16):
+        raise TypeError("router_linear_backward_f32 takes fp32 d_logits, bf16 x and weight")
+    d_logits = _contig(d_logits)
+    x = _contig(x)
+    weight = _contig(weight)
+    T, E = d_logits.shape
+    H = x.shape[1]
+    if weight.shape != (E, H):
+        raise ValueError(f"router_linear_backward_f32: weight {tuple(weight.shape)} vs ({E}, {H})")
+    lib = _lib.load()
+    nbytes = lib.moe_amd_router_linear_backward_f32_workspace_size(T, E, H)
+    ws = torch.empty(max(nbytes, 16), device=x.device, dtype=torch.uint8)
+    d_x = (torch.empty(T, H, device=x.device, dtype=torch.bfloat16) if need_x
+           else x.new_empty(0))
+    d_w = (torch.empty(E, H, device=x.device, dtype=torch.bfloat16) if need_w
+           else weight.new_empty(0))
+    _call("moe_amd_router_linear_backward_f32", d_logits.data_ptr(), x.data_ptr(),
+          weight.data_ptr(), T, E, H, ws.data_ptr(), ws.numel(),
+          d_x.data_ptr() if need_x else None, d_w.data_ptr() if need_w else None, _stream(x))
+    return d_x, d_w
+
+
 def router_linear_backward_dw(d_logits: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
     """d_weight [E,H] = bf16(d_logits [T,E]^T . x [T,H]) on MFMA, split over
-    token chunks with fp32 partials (E <= 256)."""
+    token chunks with fp32 partials."""
     _need_cuda(d_logits, x)
     if d_logits.dtype != torch.bfloat16 or x.dtype != torch.bfloat16:
         raise TypeError("router_linear_backward_dw takes bf16 d_logits and hidden states")

@@ -283,7 +283,7 @@ def test_router_linear_backward_dx_and_gather_add():
 
 
 @pytest.mark.parametrize("T,H,E", [(65536, 2048, 128), (1001, 512, 16), (37, 256, 8), (0, 256, 8),
-                                   (4096, 768, 256)])
+                                   (4096, 768, 256), (3000, 512, 1792), (700, 256, 264)])
 def test_router_linear_backward_dw(T, H, E):
     """The gating linear's weight gradient (split over token chunks, fp32
     partials) against fp32 torch on the same bf16 inputs: within one bf16
@@ -302,6 +302,54 @@ def test_router_linear_backward_dw(T, H, E):
     err = (dw.double() - ref.double()).abs()
     tol = ref.double().abs() * 2.0 ** -8 + 1e-5 * max(ref.abs().max().item(), 1.0)
     assert bool((err <= tol).all()), float((err - tol).max())
+
+
+@pytest.mark.parametrize("T,H,E,need", [(16384, 2048, 1792, "both"), (4096, 1024, 128, "both"),
+                                        (1001, 512, 32, "x"), (777, 256, 96, "w"),
+                                        (0, 256, 64, "both")])
+def test_router_linear_backward_f32(T, H, E, need):
+    """Gradients of the fp32 gating linear F.linear(h.float(), W.float()) from
+    the two-term bf16 split of d_logits on the MFMA kernels, against fp64
+    products of the same inputs: |got - exact| <= 2^-8 |exact| (the one bf16
+    rounding) + 2^-14 sum|g||w| (the split's 2^-18 residual and fp32 sums);
+    and equal to torch's fp32 GEMM + bf16 cast on >= 98% of the elements (the
+    rest sit at a bf16 rounding boundary).  A gradient not asked for is not
+    computed."""
+    print(f"router f32 backward T={T} H={H} E={E} need={need}", flush=True)
+    g = torch.Generator().manual_seed(T + H + E + 3)
+    # sigmoid-derivative-sized gradients with a wide exponent range
+    dl = (torch.randn(T, E, generator=g) * torch.rand(T, E, generator=g).pow(4) * 0.25).to(DEV)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(DEV)
+    wr = (torch.randn(E, H, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    dx, dw = ops.router_linear_backward_f32(dl, x, wr, need != "w", need != "x")
+    dx2, dw2 = ops.router_linear_backward_f32(dl, x, wr, need != "w", need != "x")
+    torch.cuda.synchronize()
+    assert torch.equal(dx, dx2) and torch.equal(dw, dw2)
+    checks = []
+    if need != "w":
+        assert dx.shape == (T, H) and dx.dtype == torch.bfloat16
+        exact = dl.double() @ wr.double()
+        scale = dl.double().abs() @ wr.double().abs()
+        fp32 = (dl @ wr.float()).to(torch.bfloat16)
+        checks.append((dx, exact, scale, fp32))
+    else:
+        assert dx.numel() == 0
+    if need != "x":
+        assert dw.shape == (E, H) and dw.dtype == torch.bfloat16
+        exact = dl.double().t() @ x.double()
+        scale = dl.double().abs().t() @ x.double().abs()
+        fp32 = (dl.t().contiguous() @ x.float()).to(torch.bfloat16)
+        checks.append((dw, exact, scale, fp32))
+    else:
+        assert dw.numel() == 0
+    for got, exact, scale, fp32 in checks:
+        err = (got.double() - exact).abs()
+        tol = exact.abs() * 2.0 ** -8 + scale * 2.0 ** -14
+        assert bool((err <= tol).all()), float((err - tol).max())
+        if got.numel():
+            assert (got == fp32).double().mean().item() >= 0.98
+    if T == 0 and need != "x":
+        assert not dw.any()
 
 
 def _sched_tables(plan, S, E):
