@@ -440,7 +440,9 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void sigmoid_topk_kernel(
     }
     if (renorm) {
       float ssum = 0.f;
-      for (int k = 0; k < K; ++k) ssum += __shfl(wk, k, 64);
+      for (int k = 0; k < K; ++k)
+        ssum += __builtin_bit_cast(float,
+                                   __builtin_amdgcn_readlane(__builtin_bit_cast(int, wk), k));
       wk = wk / (ssum + 1e-20f);
     }
     if (scaling > 0.f) wk = wk * scaling;
@@ -465,9 +467,10 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void sigmoid_topk_kernel(
 // Every lane k < K holds (v_k, g_k); returns dv_k.
 __device__ __forceinline__ float renorm_backward(float vk, float gk, int K, float eps) {
   float ssum = 0.f, gv = 0.f;
-  for (int k = 0; k < K; ++k) {
-    ssum += __shfl(vk, k, 64);
-    gv += __shfl(gk * vk, k, 64);
+  const float gvk = gk * vk;
+  for (int k = 0; k < K; ++k) {  // k is uniform: lane reads, not shuffles
+    ssum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, vk), k));
+    gv += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gvk), k));
   }
   float den = ssum + eps;
   return gk / den - gv / (den * den);
@@ -682,11 +685,17 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void sigmoid_topk_bwd_kernel(
       ds[j] = (e < E && dscores) ? dscores[t * E + e] : 0.f;
     }
     for (int k = 0; k < K; ++k) {
-      int e = __shfl(ek, k, 64);
-      float g = __shfl(dv, k, 64);
+      // the k-th routed (expert, gradient), uniform: only its owner lane
+      // adds, into the register picked by a scalar branch
+      const int e = __builtin_amdgcn_readlane(ek, k);
+      const float g = __builtin_bit_cast(float,
+                                         __builtin_amdgcn_readlane(__builtin_bit_cast(int, dv), k));
+      if (e >= 0 && e < E) {
+        const int l0 = e & 63, j0 = e >> 6;
 #pragma unroll
-      for (int j = 0; j < NV; ++j)
-        if (e == j * 64 + lane) ds[j] += g;
+        for (int j = 0; j < NV; ++j)
+          if (j == j0 && lane == l0) ds[j] += g;
+      }
     }
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
