@@ -53,6 +53,7 @@ CASES = [
     (2048, 512, 64, 8, 256, 3.0, 0, torch.float32),     # heavy skew, empty experts
     (777, 256, 32, 2, 128, 0.0, 5, torch.float32),      # ragged T, EP sentinels
     (600, 512, 256, 8, 192, 0.0, 0, torch.bfloat16),    # tiny groups, bf16 weights
+    (901, 320, 24, 3, 320, 1.0, 7, torch.float32),      # H, I, 2I not multiples of 256
 ]
 
 
