@@ -190,8 +190,8 @@ def routing_consumers(cfg, probs, dev, reps: int = 5) -> dict:
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="l")
     ap.add_argument("--cpu-tokens", type=int, default=16384)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -240,15 +240,21 @@ def main():
 
     events: list = []
     ops.record_kernel_times(events)
+    # HIP events between steps, on the stream every kernel is launched on
+    # (torch's current stream), for the per-step median next to the wall-clock mean.
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    marks[0].record()
+    for i in range(args.steps):
         idx = step()
+        marks[i + 1].record()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     ops.record_kernel_times(None)
     ms = (t1 - t0) * 1000.0 / args.steps
-    log(f"[bench] {args.steps} steps: {ms:.3f} ms/step")
+    step_ms = sorted(marks[i].elapsed_time(marks[i + 1]) for i in range(args.steps))
+    log(f"[bench] {args.steps} steps: {ms:.3f} ms/step (median {step_ms[len(step_ms) // 2]:.3f})")
 
     per: dict[str, list[float]] = {}
     for name, s, e in events:
@@ -285,6 +291,8 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 4),
+        "step_ms_events": {"median": round(step_ms[len(step_ms) // 2], 4),
+                           "min": round(step_ms[0], 4), "max": round(step_ms[-1], 4)},
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
