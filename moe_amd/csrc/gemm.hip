@@ -357,12 +357,32 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
     return make_rsrc(ptr + adv, left);
   };
   int kb_cur = 0, ke_cur = 0;
+  // RLT: each tile walks its k-stages starting at stage ct % nk (wrapping),
+  // so that the workgroups, all starting together, read different 128-byte
+  // column blocks of their token rows instead of the same block of every
+  // row at once (which lands on few HBM channels).  Other modes: identity.
+  int krot = 0, knk = 1;
+  auto kst = [&](int st) -> uint32_t {
+    if constexpr (MODE == RLT) {
+      int v = st + krot;
+      v -= v >= knk ? knk : 0;
+      v -= v >= knk ? knk : 0;
+      v -= v >= knk ? knk : 0;
+      return (uint32_t)v;
+    } else {
+      return (uint32_t)st;
+    }
+  };
   int erow_src = 0;        // G2DXF: row_src of tile row tid
   uint32_t erow_wraw = 0;  // ... and its routing weight's bits (fp32, or bf16 zero-extended)
 
   auto setup = [&](const Tile& d) {
     kb_cur = d.kbeg;
     ke_cur = d.kend;
+    if constexpr (MODE == RLT) {
+      knk = d.nk > 0 ? d.nk : 1;
+      krot = __builtin_amdgcn_readfirstlane(d.ct % knk);
+    }
     // Column operand.
     if constexpr (MODE == G1F) {
       cptr = (const char*)(p.w + (int64_t)d.e * I2 * H);
@@ -505,14 +525,14 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
   };
   auto issue_col = [&](int s, const int (&tk)[NTOK > 0 ? NTOK : 1]) {
     char* base = slot_ptr(2 * s);
-    const auto rs = stage_rsrc(cptr, cbytes, (uint32_t)s * cstep);
+    const auto rs = stage_rsrc(cptr, cbytes, kst(s) * cstep);
 #pragma unroll
     for (int i = 0; i < CPW; ++i) dma16(rs, col_off(s, i, tk), base + (wid + NW * i) * 1024);
   };
   // DMA of the row half of stage s (ring position 2s+1).
   auto issue_row = [&](int s) {
     char* base = slot_ptr(2 * s + 1);
-    const auto rs = stage_rsrc(rptr, rbytes, (uint32_t)s * rstep);
+    const auto rs = stage_rsrc(rptr, rbytes, kst(s) * rstep);
 #pragma unroll
     for (int i = 0; i < RPW; ++i) dma16(rs, roff[i], base + (wid + NW * i) * 1024);
   };
@@ -637,11 +657,11 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
                 isrc, (uint32_t)(kb_cur + (w + 3) * BK + lane) * 4, 0, 0);
         } else if (o < NTOK + RPW) {
           const int i = o - NTOK;
-          const auto rs = stage_rsrc(rptr, rbytes, (uint32_t)(w + 1) * rstep);
+          const auto rs = stage_rsrc(rptr, rbytes, kst(w + 1) * rstep);
           dma16(rs, roff[i], slot_ptr(2 * w + 3) + (wid + NW * i) * 1024);
         } else {
           const int i = o - NTOK - RPW;
-          const auto rs = stage_rsrc(cptr, cbytes, (uint32_t)(w + 2) * cstep);
+          const auto rs = stage_rsrc(cptr, cbytes, kst(w + 2) * cstep);
           dma16(rs, col_off(w + 2, i, tk), slot_ptr(2 * w + 4) + (wid + NW * i) * 1024);
         }
       };
