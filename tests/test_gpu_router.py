@@ -181,6 +181,7 @@ def test_sigmoid_router_backward_parity(E, K, wdt):
     (3000, 512, 200),     # transposed form, 256-expert row tile, ragged T
     (700, 256, 256),      # transposed form, full 256-expert row tile
     (77, 1024, 64),       # transposed form, fewer tokens than one column tile
+    (1500, 320, 96),      # transposed form, 5 k-stages: every rotated k start, wrapping
 ])
 def test_router_linear_parity(T, H, E):
     """The MFMA gating linear against fp32 torch on the same bf16 inputs: the
