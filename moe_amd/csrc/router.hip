@@ -667,7 +667,14 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void sigmoid_topk_bwd_kernel(
     const float* __restrict__ scores, const int64_t* __restrict__ idx,
     const void* __restrict__ dw, int w_dtype, const float* __restrict__ dscores, int64_t T,
     int E, int K, int renorm, float scaling, float* __restrict__ dlogits) {
+  // Per wave, an E-float LDS row that stays zero between tokens: the K routed
+  // gradients are written at their experts, read back by every entry's owner
+  // lane (one LDS read per entry instead of K compares), and cleared again.
+  extern __shared__ float routed[];
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  float* const row = routed + wid * E;
+  for (int e = lane; e < E; e += 64) row[e] = 0.f;
+  __builtin_amdgcn_wave_barrier();
   const int64_t nwaves = (int64_t)gridDim.x * kWavesPerBlock;
   for (int64_t t = (int64_t)blockIdx.x * kWavesPerBlock + wid; t < T; t += nwaves) {
     int ek = lane < K ? (int)idx[t * K + lane] : -1;
@@ -684,27 +691,23 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void sigmoid_topk_bwd_kernel(
       int e = j * 64 + lane;
       ds[j] = (e < E && dscores) ? dscores[t * E + e] : 0.f;
     }
-    for (int k = 0; k < K; ++k) {
-      // the k-th routed (expert, gradient), uniform: only its owner lane
-      // adds, into the register picked by a scalar branch
-      const int e = __builtin_amdgcn_readlane(ek, k);
-      const float g = __builtin_bit_cast(float,
-                                         __builtin_amdgcn_readlane(__builtin_bit_cast(int, dv), k));
-      if (e >= 0 && e < E) {
-        const int l0 = e & 63, j0 = e >> 6;
-#pragma unroll
-        for (int j = 0; j < NV; ++j)
-          if (j == j0 && lane == l0) ds[j] += g;
-      }
-    }
+    const bool routed_ok = lane < K && ek >= 0 && ek < E;  // top-k ids are distinct
+    if (routed_ok) row[ek] = dv;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
       int e = j * 64 + lane;
       if (e < E) {
         float y = scores[t * E + e];
-        dlogits[t * E + e] = ds[j] * (1.f - y) * y;
+        dlogits[t * E + e] = (ds[j] + row[e]) * (1.f - y) * y;
       }
     }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (routed_ok) row[ek] = 0.f;
   }
 }
 
@@ -925,7 +928,8 @@ extern "C" int moe_amd_router_sigmoid_topk_backward(const float* scores,
 #undef MOE_SIGMOID_BWD_GROUP
     return check_launch("router_sigmoid_topk_backward");
   }
-  MOE_DISPATCH_NV(E, sigmoid_topk_bwd_kernel, grid_for(T), 64 * kWavesPerBlock, 0,
+  MOE_DISPATCH_NV(E, sigmoid_topk_bwd_kernel, grid_for(T), 64 * kWavesPerBlock,
+                  (size_t)kWavesPerBlock * E * sizeof(float),
                   (hipStream_t)stream >>>(scores, topk_index, d_topk_weights, weights_dtype,
                                           d_scores, T, E, K, renormalize, scaling_factor,
                                           d_logits));
