@@ -31,6 +31,7 @@ import torch
 
 METRIC = ("MoE layer fwd+bwd tokens/sec and grouped-GEMM TFLOP/s (% bf16 MFMA peak), 1 GPU")
 PEAK_BF16_TFLOPS = 2500.0
+PEAK_FP32_TFLOPS = 157.3  # dense fp32 MFMA (the fp32 XS-standard layer's GEMMs)
 PEAK_HBM_GBS = 8000.0
 
 
@@ -69,31 +70,87 @@ def hbm_bytes(name: str, cfg) -> float:
 
 def cpu_baseline(cfg, tokens: int) -> dict:
     """The oracle (pure-torch CPU restatement of the reference layer) timed
-    for one fwd+bwd on `tokens` tokens of the same shape."""
+    for one fwd+bwd on `tokens` tokens of the workload: gating linear,
+    router, experts forward, experts backward, router backward and the
+    gating linear's two gradients.  Only the experts the sample routes to
+    are materialised (drawn before the clock starts): an expert no row
+    reaches costs the reference nothing either."""
     from oracle import moe_oracle as O
-    from moe_amd.configs import make_inputs
 
     threads = os.cpu_count() or 1
     torch.set_num_threads(threads)
     c = cfg.scaled(tokens)
-    inp = make_inputs(c, seed=0, device="cpu")
+    T, H, E, K, I, dt = c.T, c.H, c.E, c.K, c.I, c.dtype
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(T, H, generator=g).to(dt)
+    wr = (torch.randn(E, H, generator=g) * 0.02).to(dt)
+    off = bias = None
+    if c.skew:
+        off = c.skew * (torch.randperm(E, generator=g).float() + 1.0).pow(-c.zipf_s)
+    if c.bias_range:
+        bias = (torch.rand(E, generator=g) * 2.0 - 1.0) * c.bias_range
+    dout = torch.randn(T, H, generator=g).to(dt)
+
+    def route():
+        if c.router == "softmax":
+            logits = torch.nn.functional.linear(x, wr)
+            return logits, O.softmax_router(logits, K, True, off)
+        logits = torch.nn.functional.linear(x.float(), wr.float())
+        return logits, O.sigmoid_router(logits, bias, K, True, None, None, None, dt)
+
+    _, (_, _, idx0) = route()
+    used = torch.unique(idx0)
+    remap = torch.full((E,), -1, dtype=torch.int64)
+    remap[used] = torch.arange(len(used))
+    w1 = (torch.randn(len(used), 2 * I, H, generator=g) * 0.02).to(dt)
+    w2 = (torch.randn(len(used), H, I, generator=g) * 0.02).to(dt)
     t0 = time.perf_counter()
-    logits = torch.nn.functional.linear(inp.x, inp.w_router)
-    probs, w, idx = O.softmax_router(logits, c.K, True, inp.logit_offset)
-    out, cache = O.experts_forward(inp.x, idx, w, inp.gate_up_proj, inp.down_proj)
-    dx, dw, dw1, dw2, _ = O.experts_backward(cache, inp.x, w, inp.gate_up_proj, inp.down_proj,
-                                             inp.dout)
-    dl = O.softmax_router_backward(probs, idx, dw, None, True, logits.dtype)
-    _ = dl.float() @ inp.w_router.float(), dl.float().T @ inp.x.float()
-    dt = time.perf_counter() - t0
+    logits, (probs, w, idx) = route()
+    sub = remap[idx]
+    out, cache = O.experts_forward(x, sub, w, w1, w2)
+    if c.backward:
+        dx, dw, dw1, dw2, _ = O.experts_backward(cache, x, w, w1, w2, dout)
+        if c.router == "softmax":
+            dl = O.softmax_router_backward(probs, idx, dw, None, True, logits.dtype).float()
+        else:
+            dl = O.sigmoid_router_backward(probs, idx, dw, None, True, None)
+        _ = dl @ wr.float(), dl.T @ x.float()
+    dt_s = time.perf_counter() - t0
     try:
         model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo")
                      if l.startswith("model name"))
     except Exception:
         model = "unknown"
-    return {"value": tokens / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"{tokens} tokens of the {cfg.name} layer (H={c.H}, E={c.E}, K={c.K}, "
-                      f"I={c.I}, bf16-emulating fp32 math), 1 fwd+bwd, {dt:.1f} s; CPU: {model}"}
+    part = "the full batch" if tokens == cfg.T else f"a {tokens}-token sample"
+    return {"value": tokens / dt_s, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{part} of the {cfg.name} layer (H={H}, E={E}, K={K}, I={I}; "
+                      f"{len(used)} experts routed to), 1 {'fwd+bwd' if c.backward else 'fwd'} in "
+                      f"{dt_s:.1f} s, "
+                      f"{'bf16-emulating fp32' if dt == torch.bfloat16 else 'fp32'} math; "
+                      f"CPU: {model}"}
+
+
+def routing_gating_check(cfg, x, wr, inp) -> dict:
+    """Outside the timed steps: how many tokens' top-k sets differ when the
+    logits come from the MFMA gating kernel instead of torch's F.linear (the
+    reference's gating, which the default bench path uses)."""
+    from moe_amd import ops
+    with torch.no_grad():
+        sig = cfg.router == "sigmoid"
+        lt = ops.torch_gating_linear(x.detach(), wr.detach(), sig)
+        lh = ops.router_linear(x.detach(), wr.detach(),
+                               torch.float32 if sig else torch.bfloat16)
+        ids = []
+        for lg in (lt, lh):
+            if sig:
+                _, _, i = ops.router_sigmoid_topk(lg, inp.expert_bias, cfg.K, True)
+            else:
+                _, _, i = ops.router_softmax_topk(lg, cfg.K, True, inp.logit_offset)
+            ids.append(i.sort(dim=1).values)
+        diff = int((ids[0] != ids[1]).any(dim=1).sum())
+        logit_diff = int((lt != lh).sum())
+    return {"tokens": cfg.T, "hip_gating_tokens_with_other_topk_set": diff,
+            "hip_gating_logits_differing": logit_diff}
 
 
 def copy_calibration(nbytes: int) -> None:
@@ -187,13 +244,43 @@ def routing_consumers(cfg, probs, dev, reps: int = 5) -> dict:
     return out
 
 
+def kernel_table(per: dict, cfg, steps: int, peak: float):
+    """Per-entry-point averages, FLOP/s and GB/s from recorded HIP events."""
+    kernels = {}
+    gemm_ms = gemm_fl = 0.0
+    for name, ts in per.items():
+        avg = sum(ts) / len(ts)
+        fl = gemm_flops(name, cfg.S, cfg.H, cfg.I)
+        by = hbm_bytes(name, cfg)
+        k = {"launches_per_step": len(ts) / steps, "avg_ms": round(avg, 4)}
+        if fl:
+            k["tflops"] = round(fl / avg / 1e9, 1)
+            k["frac_peak"] = round(fl / avg / 1e9 / peak, 4)
+            gemm_ms += avg * len(ts) / steps
+            gemm_fl += fl * len(ts) / steps
+        if by:
+            k["gbs"] = round(by / avg / 1e6, 1)
+            k["frac_hbm"] = round(by / avg / 1e6 / PEAK_HBM_GBS, 4)
+        kernels[name.replace("moe_amd_", "")] = k
+    return kernels, gemm_ms, gemm_fl
+
+
 def main():
+    from moe_amd.library import GATINGS
+
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="l")
-    ap.add_argument("--cpu-tokens", type=int, default=16384)
+    ap.add_argument("--gating", default="torch", choices=GATINGS,
+                    help="source of the router logits: torch's F.linear (the reference's own "
+                         "call: bit-identical logits and routing) or the MFMA gating kernel")
+    ap.add_argument("--kernel-steps", type=int, default=5,
+                    help="steps of the separate per-kernel timing pass after the timed steps")
+    ap.add_argument("--cpu-tokens", type=int, default=0,
+                    help="CPU-baseline sample (0: the whole batch, or 128 tokens for banks "
+                         "over 2 GB)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain device-to-device copy of BYTES (three times): the "
@@ -214,23 +301,25 @@ def main():
 
     cfg = CONFIGS[args.config]
     dev = torch.device("cuda:0")
-    log(f"[bench] config {cfg.name}: T={cfg.T} H={cfg.H} E={cfg.E} K={cfg.K} I={cfg.I}")
-    inp = make_inputs(cfg, seed=0, device=dev,
-                      weight_device=dev if cfg.E * cfg.H * cfg.I > 2**31 else None)
+    log(f"[bench] config {cfg.name}: T={cfg.T} H={cfg.H} E={cfg.E} K={cfg.K} I={cfg.I} "
+        f"gating={args.gating}")
+    inp = make_inputs(cfg, seed=0, device=dev)
+    log("[bench] inputs drawn (CPU, BASELINE order) and resident on the GPU")
     x = inp.x.clone().requires_grad_(True)
     wr = inp.w_router.clone().requires_grad_(True)
-    w1 = inp.gate_up_proj.clone().requires_grad_(True)
-    w2 = inp.down_proj.clone().requires_grad_(True)
+    w1 = inp.gate_up_proj.requires_grad_(True)
+    w2 = inp.down_proj.requires_grad_(True)
     params = (x, wr, w1, w2)
-    router = cfg.router
+    backward = cfg.backward
 
     def step():
         for p in params:
             p.grad = None
-        out, probs, w, idx = moe_layer(x, wr, w1, w2, cfg.K, router=router,
+        out, probs, w, idx = moe_layer(x, wr, w1, w2, cfg.K, router=cfg.router,
                                        logit_offset=inp.logit_offset,
-                                       expert_bias=inp.expert_bias)
-        out.backward(inp.dout)
+                                       expert_bias=inp.expert_bias, gating=args.gating)
+        if backward:
+            out.backward(inp.dout)
         return idx
 
     for i in range(args.warmup):
@@ -238,10 +327,9 @@ def main():
         log(f"[bench] warmup {i + 1}/{args.warmup}")
     torch.cuda.synchronize()
 
-    events: list = []
-    ops.record_kernel_times(events)
+    # Timed steps: nothing but the layer (no per-kernel instrumentation);
     # HIP events between steps, on the stream every kernel is launched on
-    # (torch's current stream), for the per-step median next to the wall-clock mean.
+    # (torch's current stream), for the per-step median beside the mean.
     marks = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -251,30 +339,26 @@ def main():
         marks[i + 1].record()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    ops.record_kernel_times(None)
     ms = (t1 - t0) * 1000.0 / args.steps
     step_ms = sorted(marks[i].elapsed_time(marks[i + 1]) for i in range(args.steps))
     log(f"[bench] {args.steps} steps: {ms:.3f} ms/step (median {step_ms[len(step_ms) // 2]:.3f})")
 
+    # Separate pass: the same steps with a HIP-event pair around every
+    # kernel launch, for the per-kernel table and the roofline.
+    events: list = []
+    ops.record_kernel_times(events)
+    torch.cuda.synchronize()
+    k0 = time.perf_counter()
+    for _ in range(args.kernel_steps):
+        step()
+    torch.cuda.synchronize()
+    k_ms = (time.perf_counter() - k0) * 1000.0 / max(args.kernel_steps, 1)
+    ops.record_kernel_times(None)
     per: dict[str, list[float]] = {}
-    for name, s, e in events:
-        per.setdefault(name, []).append(s.elapsed_time(e))
-    kernels = {}
-    gemm_ms = gemm_fl = 0.0
-    for name, ts in per.items():
-        avg = sum(ts) / len(ts)
-        fl = gemm_flops(name, cfg.S, cfg.H, cfg.I)
-        by = hbm_bytes(name, cfg)
-        k = {"launches_per_step": len(ts) / args.steps, "avg_ms": round(avg, 4)}
-        if fl:
-            k["tflops"] = round(fl / avg / 1e9, 1)
-            k["frac_peak"] = round(fl / avg / 1e9 / PEAK_BF16_TFLOPS, 4)
-            gemm_ms += avg * len(ts) / args.steps
-            gemm_fl += fl * len(ts) / args.steps
-        if by:
-            k["gbs"] = round(by / avg / 1e6, 1)
-            k["frac_hbm"] = round(by / avg / 1e6 / PEAK_HBM_GBS, 4)
-        kernels[name.replace("moe_amd_", "")] = k
+    for name, s_ev, e_ev in events:
+        per.setdefault(name, []).append(s_ev.elapsed_time(e_ev))
+    peak = PEAK_BF16_TFLOPS if cfg.dtype == torch.bfloat16 else PEAK_FP32_TFLOPS
+    kernels, gemm_ms, gemm_fl = kernel_table(per, cfg, args.kernel_steps, peak)
     gemms = {n: ts for n, ts in per.items() if gemm_flops(n, cfg.S, cfg.H, cfg.I)}
     dom = max(gemms, key=lambda n: sum(gemms[n]))
     dom_avg = sum(gemms[dom]) / len(gemms[dom])
@@ -282,6 +366,7 @@ def main():
     achieved = dom_fl / dom_avg / 1e9
     counts = torch.bincount(idx.reshape(-1), minlength=cfg.E)
     imbalance = counts.max().item() / (cfg.S / cfg.E)
+    log(f"[bench] per-kernel pass: {args.kernel_steps} steps, {k_ms:.3f} ms/step")
 
     result = {
         "metric": METRIC,
@@ -296,24 +381,36 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (seeded N(0,1) inputs, N(0,0.02) random-init weights)",
-        "config": {"workload": f"{cfg.name} MoE layer fwd+bwd", "T": cfg.T, "H": cfg.H,
-                   "E": cfg.E, "K": cfg.K, "I": cfg.I, "router": cfg.router,
+        "dtype": "bf16" if cfg.dtype == torch.bfloat16 else "fp32",
+        "data": "synthetic (seeded N(0,1) inputs, N(0,0.02) random-init weights, drawn on the "
+                "CPU in the BASELINE order)",
+        "config": {"workload": f"{cfg.name} MoE layer {'fwd+bwd' if backward else 'fwd'}",
+                   "T": cfg.T, "H": cfg.H, "E": cfg.E, "K": cfg.K, "I": cfg.I,
+                   "router": cfg.router, "gating": args.gating,
                    "load_imbalance_max_over_mean": round(imbalance, 3)},
         "gemm": {"flops_per_step": gemm_fl, "ms_per_step": round(gemm_ms, 4),
                  "tflops": round(gemm_fl / gemm_ms / 1e9, 1),
-                 "frac_peak": round(gemm_fl / gemm_ms / 1e9 / PEAK_BF16_TFLOPS, 4)},
+                 "frac_peak": round(gemm_fl / gemm_ms / 1e9 / peak, 4),
+                 "timed_in": f"separate per-kernel pass of {args.kernel_steps} steps "
+                             f"({k_ms:.3f} ms/step with the events)"},
         "roofline": {"bound": "mfma", "kernel": dom.replace("moe_amd_", ""),
-                     "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "achieved": round(achieved, 1), "peak": peak,
+                     "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
                      "traffic": recorded_traffic(cfg.name, dom.replace("moe_amd_", ""))},
         "kernels": kernels,
+        "routing": dict(routing_gating_check(cfg, x, wr, inp),
+                        timed_gating=args.gating,
+                        timed_routing="bit-identical to the reference's (torch F.linear logits)"
+                        if args.gating == "torch" else "MFMA gating logits"),
     }
-    result["routing_consumers"] = routing_consumers(cfg, probs_for_consumers(cfg, x, wr, inp), dev)
+    if cfg.router == "softmax" and cfg.backward:
+        result["routing_consumers"] = routing_consumers(cfg, probs_for_consumers(cfg, x, wr, inp),
+                                                        dev)
     if not args.no_cpu_baseline:
-        log(f"[bench] CPU baseline on {args.cpu_tokens} tokens ...")
-        result["cpu_baseline"] = cpu_baseline(cfg, args.cpu_tokens)
+        big = cfg.E * 3 * cfg.H * cfg.I * 2 > 2 * 2**30
+        tokens = args.cpu_tokens or (128 if big else cfg.T)
+        log(f"[bench] CPU baseline on {tokens} tokens ...")
+        result["cpu_baseline"] = cpu_baseline(cfg, tokens)
     print(json.dumps(result), flush=True)
 
 

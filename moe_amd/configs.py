@@ -65,34 +65,24 @@ class LayerInputs:
     dout: torch.Tensor
 
 
-def make_inputs(cfg: LayerConfig, seed: int = 0, device: str | torch.device = "cpu",
-                weight_device: str | torch.device | None = None) -> LayerInputs:
+def make_inputs(cfg: LayerConfig, seed: int = 0, device: str | torch.device = "cpu"
+                ) -> LayerInputs:
     """Seeded inputs in the fixed draw order, cast to cfg.dtype on `device`.
 
-    ``weight_device`` (default: the CPU) is where the expert weights are
-    drawn; drawing them on the GPU avoids a multi-GB CPU buffer for the
-    1792-expert bank, at the cost of bits that differ from a CPU draw."""
+    Every tensor is drawn on the CPU; the expert banks one expert at a time
+    (each expert's fp32 draw is cast and copied to `device` before the next
+    is drawn), so even the 1792-expert bank needs no multi-GB host buffer
+    and a CPU and a GPU run see identical bits."""
     g = torch.Generator().manual_seed(seed)
     dt = cfg.dtype
     x = torch.randn(cfg.T, cfg.H, generator=g).to(dt).to(device)
     w_router = (torch.randn(cfg.E, cfg.H, generator=g) * 0.02).to(dt).to(device)
-    if weight_device is None or torch.device(weight_device).type == "cpu":
-        w1 = torch.empty(cfg.E, 2 * cfg.I, cfg.H, dtype=dt, device=device)
-        w2 = torch.empty(cfg.E, cfg.H, cfg.I, dtype=dt, device=device)
-        for e in range(cfg.E):  # per expert keeps the fp32 staging buffer small
-            w1[e] = (torch.randn(2 * cfg.I, cfg.H, generator=g) * 0.02).to(dt)
-        for e in range(cfg.E):
-            w2[e] = (torch.randn(cfg.H, cfg.I, generator=g) * 0.02).to(dt)
-    else:
-        gd = torch.Generator(device=weight_device).manual_seed(seed + 1)
-        w1 = torch.empty(cfg.E, 2 * cfg.I, cfg.H, dtype=dt, device=weight_device)
-        w2 = torch.empty(cfg.E, cfg.H, cfg.I, dtype=dt, device=weight_device)
-        for e in range(cfg.E):
-            w1[e] = (torch.randn(2 * cfg.I, cfg.H, generator=gd, device=weight_device)
-                     * 0.02).to(dt)
-            w2[e] = (torch.randn(cfg.H, cfg.I, generator=gd, device=weight_device)
-                     * 0.02).to(dt)
-        w1, w2 = w1.to(device), w2.to(device)
+    w1 = torch.empty(cfg.E, 2 * cfg.I, cfg.H, dtype=dt, device=device)
+    w2 = torch.empty(cfg.E, cfg.H, cfg.I, dtype=dt, device=device)
+    for e in range(cfg.E):
+        w1[e] = (torch.randn(2 * cfg.I, cfg.H, generator=g) * 0.02).to(dt)
+    for e in range(cfg.E):
+        w2[e] = (torch.randn(cfg.H, cfg.I, generator=g) * 0.02).to(dt)
     offset = bias = None
     if cfg.skew:
         rank = torch.randperm(cfg.E, generator=g).to(torch.float32) + 1.0

@@ -59,6 +59,7 @@
 #include <atomic>
 
 #include "common.h"
+#include "gemm_f32.h"
 
 namespace moe {
 namespace {
@@ -1077,8 +1078,11 @@ int launch_token(GemmArgs a, int64_t S, int E, int ncols_per_tile_out, int ncols
   return launch<MODE, 64>(a, (int)max_tiles, st);
 }
 int check_common(int64_t S, int E, int H, int I, int dtype, const char* who) {
+  MOE_REQUIRE(dtype == MOE_DTYPE_BF16 || dtype == MOE_DTYPE_F32, MOE_ERR_DTYPE,
+              "%s: dtype %d is neither bf16 nor fp32", who, dtype);
   MOE_REQUIRE(dtype == MOE_DTYPE_BF16, MOE_ERR_UNSUPPORTED,
-              "%s: only bf16 (dtype %d) is implemented on the GPU path", who, MOE_DTYPE_BF16);
+              "%s: bf16 only; fp32 layers run the unfused backward (combine_backward, "
+              "gemm_down_backward_dx_dswiglu, gemm_down_backward_dw)", who);
   MOE_REQUIRE(S >= 0 && E >= 1 && H > 0 && I > 0, MOE_ERR_ARG, "%s: bad sizes", who);
   MOE_REQUIRE(H % 64 == 0 && I % 64 == 0, MOE_ERR_ARG,
               "%s: H=%d and I=%d must be multiples of 64", who, H, I);
@@ -1108,6 +1112,10 @@ extern "C" int moe_amd_gemm_gate_up_swiglu(const void* hidden_states, const int3
                                            int64_t T, int64_t S, int E, int H, int I, int dtype,
                                            void* gate_up_out, void* act_out, void* stream) {
   const char* who = "gemm_gate_up_swiglu";
+  if (dtype == MOE_DTYPE_F32)
+    return f32_gate_up_swiglu((const float*)hidden_states, row_src, top_k, offsets, tile_plan,
+                              (const float*)gate_up_proj, T, S, E, H, I, (float*)gate_up_out,
+                              (float*)act_out, (hipStream_t)stream);
   int rc = check_common(S, E, H, I, dtype, who);
   if (rc) return rc;
   MOE_REQUIRE(top_k >= 1 && S == T * top_k, MOE_ERR_ARG, "%s: S != T*top_k", who);
@@ -1135,6 +1143,9 @@ extern "C" int moe_amd_gemm_down(const void* act, const int32_t* offsets,
                                  const void* tile_plan, const void* down_proj, int64_t S,
                                  int E, int H, int I, int dtype, void* y_out, void* stream) {
   const char* who = "gemm_down";
+  if (dtype == MOE_DTYPE_F32)
+    return f32_down((const float*)act, offsets, tile_plan, (const float*)down_proj, S, E, H, I,
+                    (float*)y_out, (hipStream_t)stream);
   int rc = check_common(S, E, H, I, dtype, who);
   if (rc) return rc;
   MOE_REQUIRE(offsets && tile_plan && down_proj && (S == 0 || (act && y_out)), MOE_ERR_ARG,
@@ -1425,6 +1436,10 @@ extern "C" int moe_amd_gemm_down_backward_dx_dswiglu(const void* dy, const int32
                                                      int64_t S, int E, int H, int I, int dtype,
                                                      void* d_gate_up, void* stream) {
   const char* who = "gemm_down_backward_dx_dswiglu";
+  if (dtype == MOE_DTYPE_F32)
+    return f32_down_dx_dswiglu((const float*)dy, offsets, tile_plan, (const float*)down_proj,
+                               (const float*)gate_up, S, E, H, I, (float*)d_gate_up,
+                               (hipStream_t)stream);
   int rc = check_common(S, E, H, I, dtype, who);
   if (rc) return rc;
   MOE_REQUIRE(offsets && tile_plan && down_proj && (S == 0 || (dy && gate_up && d_gate_up)),
@@ -1490,6 +1505,9 @@ extern "C" int moe_amd_gemm_gate_up_backward_dx(const void* d_gate_up, const int
                                                 int H, int I, int dtype, void* d_xs,
                                                 void* stream) {
   const char* who = "gemm_gate_up_backward_dx";
+  if (dtype == MOE_DTYPE_F32)
+    return f32_gate_up_dx((const float*)d_gate_up, offsets, tile_plan, (const float*)gate_up_proj,
+                          S, E, H, I, (float*)d_xs, (hipStream_t)stream);
   int rc = check_common(S, E, H, I, dtype, who);
   if (rc) return rc;
   MOE_REQUIRE(offsets && tile_plan && gate_up_proj && (S == 0 || (d_gate_up && d_xs)), MOE_ERR_ARG,
@@ -1522,6 +1540,9 @@ extern "C" int moe_amd_gemm_down_backward_dw(const void* dy, const void* act,
                                              int64_t S, int E, int H, int I, int dtype,
                                              void* d_down_proj, void* stream) {
   const char* who = "gemm_down_backward_dw";
+  if (dtype == MOE_DTYPE_F32)  // static tile walk (the schedule is for the bf16 kernels)
+    return f32_down_dw((const float*)dy, (const float*)act, offsets, S, E, H, I,
+                       (float*)d_down_proj, (hipStream_t)stream);
   int rc = check_common(S, E, H, I, dtype, who);
   if (rc) return rc;
   MOE_REQUIRE((S == 0 || (dy && act)) && offsets && d_down_proj, MOE_ERR_ARG,
@@ -1584,6 +1605,9 @@ extern "C" int moe_amd_gemm_gate_up_backward_dw(const void* d_gate_up, const voi
                                                 int64_t T, int64_t S, int E, int H, int I,
                                                 int dtype, void* d_gate_up_proj, void* stream) {
   const char* who = "gemm_gate_up_backward_dw";
+  if (dtype == MOE_DTYPE_F32)
+    return f32_gate_up_dw((const float*)d_gate_up, (const float*)hidden_states, row_src, top_k,
+                          offsets, T, S, E, H, I, (float*)d_gate_up_proj, (hipStream_t)stream);
   int rc = check_common(S, E, H, I, dtype, who);
   if (rc) return rc;
   MOE_REQUIRE(top_k >= 1 && S == T * top_k, MOE_ERR_ARG, "%s: S != T*top_k", who);

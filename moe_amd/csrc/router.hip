@@ -61,6 +61,16 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void softmax_topk_kernel(
       }
     }
     if (t + nwaves < T) fetch(t + nwaves);
+    // A NaN logit makes every prob of the row NaN, and the reference ranks
+    // the probs: the row's entries then all tie and rank by index.
+    bool nan_here = false;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) nan_here |= v[j] != v[j];
+    if (__ballot(nan_here)) {
+#pragma unroll
+      for (int j = 0; j < NV; ++j)
+        if (j * 64 + lane < E) v[j] = __builtin_nanf("");
+    }
     float m = -INFINITY;
 #pragma unroll
     for (int j = 0; j < NV; ++j) m = fmaxf(m, v[j]);
@@ -263,6 +273,19 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void softmax_topk_group_kernel
                     : -INFINITY;
           key[j] = e < E ? rank_key(v[j], e) : 0ull;
         }
+      }
+    }
+    // A NaN logit makes every prob of the row NaN, and the reference ranks
+    // the probs: the row's entries then all tie and rank by index.
+    uint32_t nan_row = 0;
+#pragma unroll
+    for (int j = 0; j < V; ++j) nan_row |= (uint32_t)(v[j] != v[j]);
+    if (group_max_key<G>(nan_row)) {
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        const int e = e0 + j;
+        if constexpr (KEY16) key[j] = e < E ? rank_key16(0x7fc0u, e) : 0u;
+        else key[j] = e < E ? rank_key(__builtin_nanf(""), e) : 0ull;
       }
     }
     float m = -INFINITY;

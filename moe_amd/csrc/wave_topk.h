@@ -1,7 +1,9 @@
 // Wave-wide top-k on wave64: the rank rule shared by the routers and the
 // routing statistics.  A wave holds one row of up to 64*NV values, value j
 // of lane L being entry j*64 + L; entries rank by value, descending, and
-// equal values by lower index.
+// equal values by lower index.  The order is total: a NaN (of either sign)
+// ranks above every number, as torch.topk places NaN first, NaNs among
+// themselves by index; -0 and +0 are equal values.
 #pragma once
 #include <type_traits>
 
@@ -11,6 +13,8 @@ namespace moe {
 
 // True when candidate (va, ea) ranks before (vb, eb).
 __device__ __forceinline__ bool ranks_before(float va, int ea, float vb, int eb) {
+  const bool na = va != va, nb = vb != vb;
+  if (na | nb) return na && (!nb || ea < eb);
   return va > vb || (va == vb && ea < eb);
 }
 
@@ -87,9 +91,10 @@ __device__ __forceinline__ int wave_topk(const float (&val)[NV], uint64_t taken,
 // an unsigned order) << 32 | (2^32 - 1 - index): larger key = ranks first,
 // so a single unsigned max implements "value descending, lower index on
 // equal values".  -0 is folded into +0 first (equal values compare by index
-// only); a NaN maps above every number (as in torch.topk).
+// only); every NaN is mapped to the positive quiet NaN first, which lands
+// above every number (as in torch.topk) whatever the NaN's sign bit.
 __device__ __forceinline__ uint64_t rank_key(float v, int idx) {
-  uint32_t b = __float_as_uint(v + 0.0f);
+  uint32_t b = v != v ? 0x7fc00000u : __float_as_uint(v + 0.0f);
   b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
   return ((uint64_t)b << 32) | (uint32_t)(0xffffffffu - (uint32_t)idx);
 }
@@ -122,6 +127,7 @@ __device__ __forceinline__ void group_steps(F&& step) {
 // the bf16 bits (value exact), one unsigned max per comparison.
 __device__ __forceinline__ uint32_t rank_key16(uint32_t bf_bits, int idx) {
   uint32_t b = bf_bits == 0x8000u ? 0u : bf_bits;  // -0 -> +0
+  if ((b & 0x7f80u) == 0x7f80u && (b & 0x7fu)) b = 0x7fc0u;  // any NaN -> +qNaN
   b = (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
   return (b << 16) | (0xffffu - (uint32_t)idx);
 }

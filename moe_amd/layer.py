@@ -2,8 +2,13 @@
 
 ``moe_layer`` is the GPU form of Qwen3MoeSparseMoeBlock.forward
 (src/models/modeling_qwen3_moe.py:284-289) with either router: flatten to
-[T,H], gating linear (MFMA kernel for bf16; ``gating="torch"`` keeps F.linear),
-HIP router kernel, HIP expert layer.
+[T,H], gating linear, HIP router kernel, HIP expert layer.  The gating
+linear's forward is torch's F.linear by default (``gating="torch"``: the very
+call the reference makes, so the logits and therefore the routing are the
+reference's, bit for bit) or the MFMA kernel (``gating="hip"``: the same
+exact bf16 products summed in the kernel's own fp32 order, so a top-k choice
+between experts whose logits tie within one bf16 rounding can differ); its
+backward runs on the MFMA kernels either way.
 ``SparseMoeBlock`` wraps it with the reference's parameter names
 (``gate.weight``, ``experts.gate_up_proj``, ``experts.down_proj``).
 """
@@ -12,7 +17,7 @@ from __future__ import annotations
 import torch
 from torch import nn
 
-from . import library  # noqa: F401  (registers the moe_amd:: ops)
+from . import library  # registers the moe_amd:: ops
 from .experts import experts_forward
 from .router import gating_linear, sigmoid_topk, softmax_topk
 
@@ -30,12 +35,12 @@ def moe_layer(x: torch.Tensor, w_router: torch.Tensor, gate_up_proj: torch.Tenso
               renormalize: bool = True, logit_offset: torch.Tensor | None = None,
               expert_bias: torch.Tensor | None = None, scaling_factor: float | None = None,
               num_groups: int | None = None, group_topk: int | None = None,
-              tokens_per_expert: torch.Tensor | None = None, gating: str = "hip"):
+              tokens_per_expert: torch.Tensor | None = None, gating: str = "torch"):
     """Returns (out [T,H], router_logits [T,E] fp32, weights [T,K], index [T,K])."""
-    if gating not in ("hip", "torch"):
-        raise ValueError(f"unknown gating {gating!r}")
+    if gating not in library.GATINGS:
+        raise ValueError(f"unknown gating {gating!r} (expected one of {library.GATINGS})")
     hip = gating == "hip"
-    if router == "softmax" and hip and _fused_softmax_ok(x, w_router, gate_up_proj, down_proj):
+    if router == "softmax" and _fused_softmax_ok(x, w_router, gate_up_proj, down_proj):
         # Gating linear + softmax router + experts as ONE autograd node (op
         # moe_amd::moe_layer_fwd), so that the two gradients of the hidden
         # states (through the gating linear and through the experts) meet
@@ -47,7 +52,7 @@ def moe_layer(x: torch.Tensor, w_router: torch.Tensor, gate_up_proj: torch.Tenso
             t.requires_grad for t in (x, w_router, gate_up_proj, down_proj))
         res = torch.ops.moe_amd.moe_layer_fwd(x.contiguous(), w_router, gate_up_proj.contiguous(),
                                               down_proj.contiguous(), int(top_k),
-                                              bool(renormalize), logit_offset, save)
+                                              bool(renormalize), logit_offset, save, gating)
         return res[0], res[1], res[2], res[3]
     if router == "softmax":
         logits = gating_linear(x, w_router, fp32=False, hip=hip)

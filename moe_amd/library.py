@@ -59,21 +59,31 @@ def _empty_like_none(t: Tensor) -> Tensor:
 
 # ------------------------------------------------------------------ experts
 
+def _saves_act_y(dtype: torch.dtype, save_for_backward: bool) -> bool:
+    # The fp32 layer's backward is the unfused one (combine backward, then
+    # GEMM-2's dX / dW from d_y): it needs act and y; bf16 recomputes act
+    # from gate_up inside its fused backward and needs neither.
+    return save_for_backward and dtype == torch.float32
+
+
 @torch.library.custom_op(f"{_LIB}::experts_fwd", mutates_args=())
 def experts_fwd(hidden_states: Tensor, top_k_index: Tensor, top_k_weights: Tensor,
                 gate_up_proj: Tensor, down_proj: Tensor, save_for_backward: bool
-                ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
-    """(out [T,H], gate_up [S,2I] or [0,2I], counts, offsets, row_src, slot,
-    tile_plan).  transformers/integrations/moe.py:377-478."""
+                ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor,
+                           Tensor]:
+    """(out [T,H], gate_up [S,2I] or [0,2I], act [S,I] and y [S,H] (fp32
+    with save_for_backward; else [0,I], [0,H]), counts, offsets, row_src,
+    slot, tile_plan).  transformers/integrations/moe.py:377-478."""
     plan = ops.permute(top_k_index, gate_up_proj.shape[0])
     gu, act = ops.gemm_gate_up_swiglu(hidden_states, plan, gate_up_proj,
                                       save_gate_up=save_for_backward)
     y = ops.gemm_down(act, plan, down_proj)
-    del act
     out = ops.combine(y, plan, top_k_weights)
+    if not _saves_act_y(hidden_states.dtype, save_for_backward):
+        act, y = act.new_empty(0, act.shape[1]), y.new_empty(0, y.shape[1])
     if gu is None:
         gu = hidden_states.new_empty(0, gate_up_proj.shape[1])
-    return out, gu, plan.counts, plan.offsets, plan.row_src, plan.slot, plan.tile_plan
+    return out, gu, act, y, plan.counts, plan.offsets, plan.row_src, plan.slot, plan.tile_plan
 
 
 @experts_fwd.register_fake
@@ -83,19 +93,40 @@ def _(hidden_states, top_k_index, top_k_weights, gate_up_proj, down_proj, save_f
     E, I2 = gate_up_proj.shape[0], gate_up_proj.shape[1]
     out = hidden_states.new_empty(T, H)
     gu = hidden_states.new_empty(S if save_for_backward else 0, I2)
-    return (out, gu) + _plan_fake(S, E, hidden_states.device)
+    sa = S if _saves_act_y(hidden_states.dtype, save_for_backward) else 0
+    act, y = hidden_states.new_empty(sa, I2 // 2), hidden_states.new_empty(sa, H)
+    return (out, gu, act, y) + _plan_fake(S, E, hidden_states.device)
+
+
+def _experts_bwd_f32(d_out, x, w, w1, w2, gu, act, y, plan, need_x, need_w1, need_w2):
+    """fp32: the reference's autograd chain kernel by kernel (combine
+    backward -> GEMM-2 dX + dSwiGLU, GEMM-2 dW -> GEMM-1 dW, dX -> gather
+    backward), every product and sum in fp32."""
+    dy, dw = ops.combine_backward(d_out, y, plan, w)
+    d_gu = ops.gemm_down_backward_dx_dswiglu(dy, plan, w2, gu)
+    d_w2 = ops.gemm_down_backward_dw(dy, act, plan, w2.shape) if need_w2 else w2.new_empty(0)
+    del dy
+    d_w1 = (ops.gemm_gate_up_backward_dw(d_gu, x, plan, w1.shape) if need_w1
+            else w1.new_empty(0))
+    d_x = (ops.gather_backward(ops.gemm_gate_up_backward_dx(d_gu, plan, w1), plan) if need_x
+           else x.new_empty(0))
+    return d_x, dw, d_w1, d_w2
 
 
 @torch.library.custom_op(f"{_LIB}::experts_bwd", mutates_args=())
 def experts_bwd(d_out: Tensor, hidden_states: Tensor, top_k_weights: Tensor, gate_up_proj: Tensor,
-                down_proj: Tensor, gate_up: Tensor, counts: Tensor, offsets: Tensor,
-                row_src: Tensor, slot: Tensor, tile_plan: Tensor, need_x: bool, need_w1: bool,
-                need_w2: bool) -> tuple[Tensor, Tensor, Tensor, Tensor]:
-    """(d_x, d_topk_weights, d_gate_up_proj, d_down_proj); the combine's
-    backward runs fused into GEMM-2's (formulas integrations/moe.py:226-242)."""
+                down_proj: Tensor, gate_up: Tensor, act: Tensor, y: Tensor, counts: Tensor,
+                offsets: Tensor, row_src: Tensor, slot: Tensor, tile_plan: Tensor, need_x: bool,
+                need_w1: bool, need_w2: bool) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """(d_x, d_topk_weights, d_gate_up_proj, d_down_proj) (formulas
+    integrations/moe.py:226-242).  bf16: the combine's backward runs fused
+    into GEMM-2's; fp32: the unfused chain on the saved act and y."""
     T, K = top_k_weights.shape
     plan = _plan(counts, offsets, row_src, slot, tile_plan, gate_up_proj.shape[0], K, T)
     d_out = d_out.to(hidden_states.dtype).contiguous()
+    if hidden_states.dtype == torch.float32:
+        return _experts_bwd_f32(d_out, hidden_states, top_k_weights.contiguous(), gate_up_proj,
+                                down_proj, gate_up, act, y, plan, need_x, need_w1, need_w2)
     d_gu, act_w, dw = ops.gemm_down_backward_fused(d_out, plan, down_proj, gate_up, top_k_weights)
     d_w2 = (ops.gemm_down_backward_dw_gathered(d_out, act_w, plan, down_proj.shape)
             if need_w2 else _empty_like_none(down_proj))
@@ -110,8 +141,8 @@ def experts_bwd(d_out: Tensor, hidden_states: Tensor, top_k_weights: Tensor, gat
 
 
 @experts_bwd.register_fake
-def _(d_out, hidden_states, top_k_weights, gate_up_proj, down_proj, gate_up, counts, offsets,
-      row_src, slot, tile_plan, need_x, need_w1, need_w2):
+def _(d_out, hidden_states, top_k_weights, gate_up_proj, down_proj, gate_up, act, y, counts,
+      offsets, row_src, slot, tile_plan, need_x, need_w1, need_w2):
     return (torch.empty_like(hidden_states) if need_x else hidden_states.new_empty(0),
             torch.empty_like(top_k_weights),
             torch.empty_like(gate_up_proj) if need_w1 else gate_up_proj.new_empty(0),
@@ -120,8 +151,8 @@ def _(d_out, hidden_states, top_k_weights, gate_up_proj, down_proj, gate_up, cou
 
 def _experts_setup(ctx, inputs, output):
     x, _, w, w1, w2, _ = inputs
-    _, gu, counts, offsets, row_src, slot, tile_plan = output
-    ctx.save_for_backward(x, w, w1, w2, gu, counts, offsets, row_src, slot, tile_plan)
+    _, gu, act, y, counts, offsets, row_src, slot, tile_plan = output
+    ctx.save_for_backward(x, w, w1, w2, gu, act, y, counts, offsets, row_src, slot, tile_plan)
 
 
 def _experts_backward(ctx, d_out, *unused):
@@ -335,16 +366,33 @@ torch.library.register_autograd(f"{_LIB}::sigmoid_topk", _sigmoid_backward,
 
 # ------------------------------------------------ softmax layer, one node
 
+GATINGS = ("torch", "hip")
+
+
+def gating_logits(x: Tensor, w_router: Tensor, gating: str, fp32: bool) -> Tensor:
+    """Router logits from the gating source ``gating``: "torch" = the
+    reference's F.linear on this device (bit-identical logits, hence the
+    reference's routing), "hip" = the MFMA gating-linear kernel (same exact
+    products, its own fp32 summation order)."""
+    if gating == "torch":
+        return ops.torch_gating_linear(x, w_router, fp32)
+    if gating == "hip":
+        return ops.router_linear(x, w_router, torch.float32 if fp32 else torch.bfloat16)
+    raise ValueError(f"unknown gating {gating!r} (expected one of {GATINGS})")
+
+
 @torch.library.custom_op(f"{_LIB}::moe_layer_fwd", mutates_args=())
 def moe_layer_fwd(x: Tensor, w_router: Tensor, gate_up_proj: Tensor, down_proj: Tensor,
                   top_k: int, renormalize: bool, logit_offset: Optional[Tensor],
-                  save_for_backward: bool
+                  save_for_backward: bool, gating: str
                   ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor,
                              Tensor, Tensor]:
     """(out, probs fp32, weights fp32, index, gate_up, counts, offsets, row_src,
-    slot, tile_plan): bf16 gating linear (MFMA), softmax router, experts
-    (Qwen3MoeSparseMoeBlock.forward, src/models/modeling_qwen3_moe.py:284-289)."""
-    logits = ops.router_linear(x, w_router, torch.bfloat16)
+    slot, tile_plan): bf16 gating linear (source ``gating``), softmax router,
+    experts (Qwen3MoeSparseMoeBlock.forward, src/models/modeling_qwen3_moe.py:
+    284-289).  The backward runs the gating linear's gradients on the MFMA
+    kernels whichever source computed the logits."""
+    logits = gating_logits(x, w_router, gating, fp32=False)
     probs, w, idx = ops.router_softmax_topk(logits, top_k, renormalize, logit_offset)
     del logits
     plan = ops.permute(idx, gate_up_proj.shape[0])
@@ -359,7 +407,8 @@ def moe_layer_fwd(x: Tensor, w_router: Tensor, gate_up_proj: Tensor, down_proj: 
 
 
 @moe_layer_fwd.register_fake
-def _(x, w_router, gate_up_proj, down_proj, top_k, renormalize, logit_offset, save_for_backward):
+def _(x, w_router, gate_up_proj, down_proj, top_k, renormalize, logit_offset, save_for_backward,
+      gating):
     T, H = x.shape
     E, I2 = gate_up_proj.shape[0], gate_up_proj.shape[1]
     S = T * top_k
@@ -416,7 +465,7 @@ def _(d_out, d_probs, d_w, x, w_router, gate_up_proj, down_proj, gate_up, probs,
 
 
 def _layer_setup(ctx, inputs, output):
-    x, w_router, gate_up_proj, down_proj, _, renormalize, _, _ = inputs
+    x, w_router, gate_up_proj, down_proj, _, renormalize, _, _, _ = inputs
     _, probs, w, idx, gu, counts, offsets, row_src, slot, tile_plan = output
     ctx.set_materialize_grads(False)
     ctx.mark_non_differentiable(idx)
@@ -428,12 +477,12 @@ def _layer_setup(ctx, inputs, output):
 def _layer_backward(ctx, d_out, d_probs, d_w, *unused):
     need_x, need_wr, need_w1, need_w2 = (bool(n) for n in ctx.needs_input_grad[:4])
     if d_out is None and d_probs is None and d_w is None:
-        return (None,) * 8
+        return (None,) * 9
     d_x, d_wr, d_w1, d_w2 = torch.ops.moe_amd.moe_layer_bwd(
         d_out, d_probs, d_w, *ctx.saved_tensors, ctx.renormalize, need_x, need_wr, need_w1,
         need_w2)
     return (d_x if need_x else None, d_wr if need_wr else None, d_w1 if need_w1 else None,
-            d_w2 if need_w2 else None, None, None, None, None)
+            d_w2 if need_w2 else None, None, None, None, None, None)
 
 
 torch.library.register_autograd(f"{_LIB}::moe_layer_fwd", _layer_backward,

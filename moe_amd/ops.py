@@ -28,16 +28,20 @@ def record_kernel_times(events: list | None) -> None:
     _events = events
 
 
-def _call(name: str, *args) -> None:
+def _timed(name: str, fn, *args):
     if _events is None:
-        _lib.call(name, *args)
-        return
+        return fn(*args)
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record()
-    _lib.call(name, *args)
+    res = fn(*args)
     end.record()
     _events.append((name, start, end))
+    return res
+
+
+def _call(name: str, *args) -> None:
+    _timed(name, _lib.call, name, *args)
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -69,6 +73,19 @@ def _contig(t: torch.Tensor) -> torch.Tensor:
 
 
 # ----------------------------------------------------------------- router
+
+def torch_gating_linear(x: torch.Tensor, weight: torch.Tensor, fp32: bool) -> torch.Tensor:
+    """The reference's own gating linear, as torch computes it on this device:
+    ``F.linear(x, W)`` (bf16 logits, src/models/modeling_qwen3_moe.py:268-270)
+    or ``F.linear(x.float(), W.float())`` (src/models/router.py:107-109).
+    Routing decided on these logits is the reference's routing bit for bit;
+    recorded as ``torch_gating_linear`` by record_kernel_times()."""
+    def run(a, b):
+        if fp32:
+            return torch.nn.functional.linear(a.float(), b.float())
+        return torch.nn.functional.linear(a, b)
+    return _timed("torch_gating_linear", run, x, weight)
+
 
 def router_linear(x: torch.Tensor, weight: torch.Tensor,
                   out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:

@@ -14,10 +14,9 @@ from __future__ import annotations
 from types import SimpleNamespace
 
 import torch
-import torch.nn.functional as F
 from torch import nn
 
-from . import library  # noqa: F401  (registers the moe_amd:: ops)
+from . import library, ops  # noqa: F401  (library registers the moe_amd:: ops)
 
 try:  # the plug-in base class of the reference's routers
     from transformers.models.qwen3_moe.modeling_qwen3_moe import Qwen3MoeTopKRouter as _RouterBase
@@ -49,9 +48,7 @@ def gating_linear(x: torch.Tensor, weight: torch.Tensor, fp32: bool, hip: bool =
     if (hip and x.is_cuda and x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16
             and H % 64 == 0 and E % 8 == 0):
         return router_linear(x, weight, torch.float32 if fp32 else torch.bfloat16)
-    if fp32:
-        return F.linear(x.float(), weight.float())
-    return F.linear(x, weight)
+    return ops.torch_gating_linear(x, weight, fp32)
 
 
 def softmax_topk(logits: torch.Tensor, top_k: int, renormalize: bool = True,

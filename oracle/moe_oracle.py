@@ -51,9 +51,13 @@ TILE_SIZES = (64, 128, 256)
 
 def rank_topk(values: torch.Tensor, k: int) -> tuple[torch.Tensor, torch.Tensor]:
     """Top-k along the last dim, sorted descending; equal values keep the
-    lower index first (a stable sort of -values).  Returns (values, index)."""
+    lower index first (a stable sort of -values; -0 == +0).  A NaN ranks
+    above every number, as torch.topk places it, NaNs among themselves by
+    index.  Returns (values, index)."""
     v = values.detach().cpu().numpy()
-    order = np.argsort(-v, axis=-1, kind="stable")[..., :k]
+    nan = np.isnan(v)
+    # lexsort: last key is primary; both sorts are stable
+    order = np.lexsort((np.where(nan, 0.0, -v), ~nan), axis=-1)[..., :k]
     idx = torch.from_numpy(np.ascontiguousarray(order)).to(torch.int64)
     return torch.gather(values.cpu(), -1, idx), idx
 

@@ -63,8 +63,15 @@ def test_abi_version_and_error_text(built_lib):
     assert "E=0" in _lib.last_error()
     rc = lib.moe_amd_gemm_down(None, None, None, None, 16, 4, 100, 64, 1, None, None)
     assert rc == -1 and "multiples of 64" in _lib.last_error()
+    # fp32 is a supported GEMM dtype (its own kernels): the null pointers are the error
     rc = lib.moe_amd_gemm_down(None, None, None, None, 16, 4, 128, 64, 0, None, None)
-    assert rc == -6 and "bf16" in _lib.last_error()
+    assert rc == -1 and "null pointer" in _lib.last_error() and "fp32" in _lib.last_error()
+    rc = lib.moe_amd_gemm_down(None, None, None, None, 16, 4, 128, 64, 7, None, None)
+    assert rc == -2 and "neither bf16 nor fp32" in _lib.last_error()
+    # the fused combine + GEMM-2 backward is bf16 only
+    rc = lib.moe_amd_gemm_down_backward_dx_fused(None, None, 2, None, None, None, None, None, 0,
+                                                 8, 16, 4, 128, 64, 0, None, None, None, None)
+    assert rc == -6 and "bf16 only" in _lib.last_error()
 
 
 def _tiny_model():
@@ -194,4 +201,95 @@ def test_shared_bank_accumulates_gradients_across_layers():
         acc2 += dw2.double()
     e1 = (w1d.grad.double().cpu() - acc1).abs().max() / acc1.abs().max()
     e2 = (w2d.grad.double().cpu() - acc2).abs().max() / acc2.abs().max()
+    assert e1 < 2e-2 and e2 < 2e-2
+
+
+@pytest.mark.gpu
+def test_global_bank_dispatches_through_experts_interface():
+    """The global shared bank as the reference builds it (src/models/
+    global_moe.py:45-66, :130-151), from transformers classes only: one
+    Qwen3MoeExperts owned by a Qwen3MoeModel and called by two router-only
+    blocks (a Qwen3MoeTopKRouter each).  After hf.install() both calls
+    dispatch through the "mi355x" ExpertsInterface key (counted), the gates
+    are the HIP routers, and the bank's dW is the oracle's sum over both
+    calls."""
+    import copy
+    from unittest import mock
+    from transformers import Qwen3MoeConfig
+    from transformers.models.qwen3_moe.modeling_qwen3_moe import (Qwen3MoeExperts, Qwen3MoeModel,
+                                                                  Qwen3MoeTopKRouter)
+    from oracle import moe_oracle as O
+    from moe_amd import experts as experts_mod
+    from moe_amd import hf
+    from moe_amd.router import MI355XTopKRouter
+
+    cfg = Qwen3MoeConfig(vocab_size=64, hidden_size=256, intermediate_size=256,
+                         moe_intermediate_size=128, num_hidden_layers=2, num_attention_heads=2,
+                         num_key_value_heads=1, head_dim=64, num_experts=32,
+                         num_experts_per_tok=4, norm_topk_prob=True,
+                         max_position_embeddings=64)
+
+    class RouterOnlyBlock(nn.Module):  # global_moe.py:45-66, restated
+        def __init__(self, config):
+            super().__init__()
+            self.gate = Qwen3MoeTopKRouter(config)
+
+        def forward(self, hidden_states, global_experts):
+            B, T, H = hidden_states.shape
+            flat = hidden_states.view(-1, H)
+            _, routing_weights, selected_experts = self.gate(flat)
+            return global_experts(flat, selected_experts, routing_weights).reshape(B, T, H)
+
+    dense = copy.deepcopy(cfg)
+    dense.mlp_only_layers = list(range(cfg.num_hidden_layers))
+    torch.manual_seed(0)
+    model = Qwen3MoeModel(dense)
+    model.config = cfg
+    model.global_experts = Qwen3MoeExperts(cfg)  # one bank, registered once (:138)
+    for layer in model.layers:
+        layer.mlp = RouterOnlyBlock(cfg)
+    with torch.no_grad():
+        for n, p in model.named_parameters():
+            if "global_experts" in n or "gate.weight" in n:
+                p.normal_(0, 0.02)
+    model = model.to("cuda", torch.bfloat16)
+    hf.install(model)
+    bank = model.global_experts
+    assert bank.config._experts_implementation == "mi355x"
+    assert all(isinstance(layer.mlp.gate, MI355XTopKRouter) for layer in model.layers)
+
+    g = torch.Generator().manual_seed(3)
+    B, T, H, K = 2, 64, cfg.hidden_size, cfg.num_experts_per_tok
+    hs = [torch.randn(B, T, H, generator=g).to(torch.bfloat16) for _ in range(2)]
+    ds = [torch.randn(B, T, H, generator=g).to(torch.bfloat16) for _ in range(2)]
+    calls = []
+    real = experts_mod.experts_forward
+
+    def counting(*a, **k):
+        calls.append(a[0].shape)
+        return real(*a, **k)
+
+    with mock.patch.object(experts_mod, "experts_forward", counting):
+        loss = 0
+        for layer, h, d in zip(model.layers, hs, ds):
+            out = layer.mlp(h.cuda(), bank)
+            loss = loss + (out.float() * d.cuda().float()).sum()
+        loss.backward()
+    torch.cuda.synchronize()
+    assert len(calls) == 2, "each router-only block's call must dispatch through mi355x"
+    w1c = bank.gate_up_proj.detach().cpu()
+    w2c = bank.down_proj.detach().cpu()
+    acc1 = torch.zeros(w1c.shape, dtype=torch.float64)
+    acc2 = torch.zeros(w2c.shape, dtype=torch.float64)
+    for layer, h, d in zip(model.layers, hs, ds):
+        flat = h.reshape(-1, H)
+        logits = torch.nn.functional.linear(flat.cuda(), layer.mlp.gate.weight).cpu()
+        _, w, idx = O.softmax_router(logits, K)
+        _, cache = O.experts_forward(flat, idx, w, w1c, w2c)
+        _, _, dw1, dw2, _ = O.experts_backward(cache, flat, w, w1c, w2c, d.reshape(-1, H))
+        acc1 += dw1.double()
+        acc2 += dw2.double()
+    e1 = (bank.gate_up_proj.grad.double().cpu() - acc1).abs().max() / acc1.abs().max()
+    e2 = (bank.down_proj.grad.double().cpu() - acc2).abs().max() / acc2.abs().max()
+    print(f"global bank dW over two calls: {e1:.2e} {e2:.2e}", flush=True)
     assert e1 < 2e-2 and e2 < 2e-2

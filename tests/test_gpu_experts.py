@@ -246,7 +246,7 @@ def test_fused_softmax_layer_matches_composed_nodes():
         w1 = inp.gate_up_proj.clone().requires_grad_(True)
         w2 = inp.down_proj.clone().requires_grad_(True)
         if fused:
-            out, probs, w, idx = moe_layer(x, wr, w1, w2, cfg.K)
+            out, probs, w, idx = moe_layer(x, wr, w1, w2, cfg.K, gating="hip")
         else:
             logits = router_linear(x, wr, torch.bfloat16)
             probs, w, idx = softmax_topk(logits, cfg.K, True, None)

@@ -56,10 +56,11 @@ def test_opcheck_routers():
                           (f32, bias, 4, True, 0.0, 0, 0, torch.bfloat16, True), test_utils=UTILS)
 
 
-def test_opcheck_layer():
-    print("opcheck moe_layer_fwd", flush=True)
+@pytest.mark.parametrize("gating", ["torch", "hip"])
+def test_opcheck_layer(gating):
+    print(f"opcheck moe_layer_fwd gating={gating}", flush=True)
     x, wr, w1, w2, *_ = _inputs()
-    args = tuple(t.requires_grad_(True) for t in (x, wr, w1, w2)) + (4, True, None, True)
+    args = tuple(t.requires_grad_(True) for t in (x, wr, w1, w2)) + (4, True, None, True, gating)
     torch.library.opcheck(torch.ops.moe_amd.moe_layer_fwd.default, args, test_utils=UTILS)
 
 

@@ -226,3 +226,40 @@ def test_router_linear_zero_tokens():
     dw = ops.router_linear_backward_dw(dl, x)
     torch.cuda.synchronize()
     assert dw.shape == (16, 256) and not dw.any()
+
+
+@pytest.mark.parametrize("router", ["softmax", "sigmoid"])
+@pytest.mark.parametrize("E,K,dtype", [(128, 8, torch.bfloat16), (1792, 8, torch.float32),
+                                       (600, 6, torch.bfloat16)])
+def test_router_nan_rows(router, E, K, dtype):
+    """Rows holding NaN logits (of either sign) route exactly as the oracle:
+    valid expert ids always (never a placeholder), NaN ranked above every
+    number; for the softmax router a NaN makes the whole prob row NaN, so
+    the K lowest ids are chosen; on the E > 256 wave-per-token kernels as on
+    the group kernels."""
+    print(f"NaN rows {router} E={E} K={K} {dtype}", flush=True)
+    g = torch.Generator().manual_seed(E + K)
+    T = 64
+    logits = torch.randn(T, E, generator=g)
+    logits[3, 7] = float("nan")
+    logits[5, E - 1] = -float("nan")
+    logits[9, :] = float("nan")
+    logits[11, ::2] = float("nan")
+    if router == "softmax":
+        lg = logits.to(dtype).to(DEV)
+        probs, w, idx = ops.router_softmax_topk(lg, K, True)
+        p_ref, w_ref, i_ref = O.softmax_router(lg.cpu(), K)
+    else:
+        lg = logits.to(DEV)
+        bias = ((torch.rand(E, generator=g) * 2 - 1) * 0.5).to(DEV)
+        probs, w, idx = ops.router_sigmoid_topk(lg, bias, K, True, None, None, None,
+                                                torch.float32)
+        p_ref, w_ref, i_ref = O.sigmoid_router(lg.cpu(), bias.cpu(), K)
+    torch.cuda.synchronize()
+    ic = idx.cpu()
+    assert bool(((ic >= 0) & (ic < E)).all()), "invalid expert id"
+    assert torch.equal(ic, i_ref)
+    nan_rows = torch.isnan(logits).any(-1)
+    assert torch.equal(torch.isnan(w.cpu()).any(-1), nan_rows)
+    ok = ~nan_rows
+    assert torch.allclose(w.cpu()[ok], w_ref[ok], rtol=1e-5, atol=1e-7)

@@ -38,21 +38,27 @@ def test_fake_shapes():
     S = T * K
     with FakeTensorMode():
         x, idx, w, w1, w2 = _inputs(T, H, E, K, I)
-        out, gu, counts, offsets, row_src, slot, plan = torch.ops.moe_amd.experts_fwd(
+        out, gu, act, y, counts, offsets, row_src, slot, plan = torch.ops.moe_amd.experts_fwd(
             x, idx, w, w1, w2, True)
         assert out.shape == (T, H) and out.dtype == torch.bfloat16
         assert gu.shape == (S, 2 * I)
+        assert act.shape == (0, I) and y.shape == (0, H)  # bf16: the fused backward needs neither
         assert counts.shape == (E,) and offsets.shape == (E + 1,) and row_src.shape == (S,)
         assert slot.shape == (S,) and counts.dtype == torch.int32
         assert plan.dtype == torch.uint8 and plan.shape[0] == _lib.load().moe_amd_tile_plan_size(S, E)
         _, gu0, *_ = torch.ops.moe_amd.experts_fwd(x, idx, w, w1, w2, False)
         assert gu0.shape == (0, 2 * I)
+        xf, w1f, w2f = x.float(), w1.float(), w2.float()
+        _, guf, actf, yf, *_ = torch.ops.moe_amd.experts_fwd(xf, idx, w, w1f, w2f, True)
+        assert guf.shape == (S, 2 * I) and actf.shape == (S, I) and yf.shape == (S, H)
+        assert actf.dtype == torch.float32  # fp32 saves act and y for its unfused backward
         dx, dw, dw1, dw2 = torch.ops.moe_amd.experts_bwd(
-            out, x, w, w1, w2, gu, counts, offsets, row_src, slot, plan, True, False, True)
+            out, x, w, w1, w2, gu, act, y, counts, offsets, row_src, slot, plan, True, False,
+            True)
         assert dx.shape == x.shape and dw.shape == w.shape and dw1.numel() == 0
         assert dw2.shape == w2.shape
         wr = torch.empty(E, H, dtype=torch.bfloat16)
-        res = torch.ops.moe_amd.moe_layer_fwd(x, wr, w1, w2, K, True, None, True)
+        res = torch.ops.moe_amd.moe_layer_fwd(x, wr, w1, w2, K, True, None, True, "hip")
         assert [tuple(r.shape) for r in res[:5]] == [(T, H), (T, E), (T, K), (T, K), (S, 2 * I)]
         assert res[1].dtype == torch.float32 and res[3].dtype == torch.int64
         logits = torch.ops.moe_amd.router_linear(x, wr, torch.float32)

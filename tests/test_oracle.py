@@ -27,6 +27,23 @@ def test_rank_topk_known_answer():
     assert vals.tolist() == [[3.0, 3.0, 3.0], [5.0, 5.0, 0.0]]
 
 
+def test_rank_topk_nan_and_signed_zero_known_answer():
+    """torch.topk places NaN above every number (either sign bit); NaNs among
+    themselves and -0 / +0 keep index order (hand-derived)."""
+    nan = float("nan")
+    v = torch.tensor([[1.0, nan, 3.0, -0.0, 0.0, float("inf"), -nan, -2.0]])
+    vals, idx = O.rank_topk(v, 8)
+    assert idx.tolist() == [[1, 6, 5, 2, 0, 3, 4, 7]]
+    # softmax router: a NaN logit makes the whole prob row NaN -> all entries
+    # tie -> the K lowest indices
+    logits = torch.tensor([[0.5, 2.0, nan, -1.0, 3.0, 0.0]])
+    p, w, i = O.softmax_router(logits, 3)
+    assert torch.isnan(p).all() and i.tolist() == [[0, 1, 2]] and torch.isnan(w).all()
+    # sigmoid router: only that score is NaN, and it ranks first
+    s, w, i = O.sigmoid_router(logits, None, 3)
+    assert i.tolist() == [[2, 4, 1]]
+
+
 def test_rank_topk_brute_force_with_ties():
     g = torch.Generator().manual_seed(1)
     v = torch.randint(0, 4, (200, 9), generator=g).float()
