@@ -142,12 +142,11 @@ __global__ __launch_bounds__(64) void tile_info_kernel(const int* __restrict__ o
     info[t] = make_int4(e, r0 + (t - t0) * bm, r1, 0);
 }
 
-// Single block: the dW-GEMM schedule.  Experts are sorted by an estimate of
-// their dW tile cost (rows + a fixed epilogue cost, in 64 log-spaced buckets,
-// heaviest first; order within a bucket is arbitrary: it changes which
-// workgroup computes a tile, never its result), then dealt to the 8 XCDs in
-// serpentine order (0..7, 7..0, ...), which balances the XCDs' sums.  Also
-// zeroes the GEMMs' queue counters.
+// Single block of 1024 threads: the dW-GEMM schedule.  Experts are sorted
+// by an estimate of their dW tile cost (rows + a fixed epilogue cost, in 64
+// log-spaced buckets, heaviest first; by expert id within a bucket), then
+// dealt to the 8 XCDs in serpentine order (0..7, 7..0, ...), which balances
+// the XCDs' sums.  Also zeroes the GEMMs' queue counters.
 __global__ __launch_bounds__(1024) void dw_schedule_kernel(const int* __restrict__ counts, int E,
                                                            int* __restrict__ queue,
                                                            int* __restrict__ xstart,
@@ -183,17 +182,51 @@ __global__ __launch_bounds__(1024) void dw_schedule_kernel(const int* __restrict
     }
   }
   __syncthreads();
+  // Rank of each expert, heaviest bucket first: its bucket's start plus the
+  // number of lower-id experts in the same bucket -- a stable counting sort,
+  // so every call writes the same schedule.  Experts go 1024 at a time (one
+  // per thread); inside a wave the lanes that share a bucket are found by
+  // one ballot per bucket bit, and the waves' per-bucket counts are added
+  // in wave order.
+  __shared__ int wcnt[16][64];  // per-wave per-bucket counts of the current 1024 experts
+  const int lane = tid & 63, wid = tid >> 6;
+  const uint64_t lt_mask = lane == 0 ? 0ull : (~0ull >> (64 - lane));
   const int rounds = E / 8, rem = E % 8;
-  for (int e = tid; e < E; e += blockDim.x) {
-    const int pos = atomicAdd(&hist[bucket(counts[e])], 1);  // rank, heaviest first
-    const int r = pos / 8, l = pos % 8;
-    const int x = (r & 1) ? 7 - l : l;
-    int start = 0;
-    for (int y = 0; y < x; ++y) {
-      const int ly = (rounds & 1) ? 7 - y : y;
-      start += rounds + (ly < rem ? 1 : 0);
+  for (int base = 0; base < E; base += 1024) {
+    for (int i = tid; i < 16 * 64; i += blockDim.x) wcnt[i >> 6][i & 63] = 0;
+    __syncthreads();
+    const int e = base + tid;
+    const bool valid = e < E;
+    const int b = valid ? bucket(counts[e]) : 0;
+    uint64_t peers = __ballot(valid);
+    for (int bit = 0; bit < 6; ++bit) {
+      const uint64_t m = __ballot((b >> bit) & 1);
+      peers &= ((b >> bit) & 1) ? m : ~m;
     }
-    xorder[start + r] = e;
+    if (valid && (peers >> lane) == 1ull) wcnt[wid][b] = __popcll(peers);  // highest peer
+    __syncthreads();
+    int pos = 0;
+    if (valid) {
+      pos = hist[b] + __popcll(peers & lt_mask);
+      for (int w = 0; w < wid; ++w) pos += wcnt[w][b];
+    }
+    __syncthreads();  // every rank is formed before the bucket starts move on
+    if (tid < 64) {
+      int tot = 0;
+      for (int w = 0; w < 16; ++w) tot += wcnt[w][tid];
+      hist[tid] += tot;
+    }
+    if (valid) {
+      const int r = pos / 8, l = pos % 8;
+      const int x = (r & 1) ? 7 - l : l;
+      int start = 0;
+      for (int y = 0; y < x; ++y) {
+        const int ly = (rounds & 1) ? 7 - y : y;
+        start += rounds + (ly < rem ? 1 : 0);
+      }
+      xorder[start + r] = e;
+    }
+    __syncthreads();
   }
 }
 
