@@ -172,6 +172,21 @@ int moe_amd_permute(const int64_t* topk_index, int64_t S, int E, void* workspace
                     size_t workspace_bytes, int32_t* counts, int32_t* offsets, int32_t* row_src,
                     int32_t* slot, void* tile_plan, size_t tile_plan_bytes, void* stream);
 
+/* moe_amd_permute without a workspace argument and without any device
+ * allocation.  No counterpart in the reference: it is for callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same outputs, bit for bit, as
+ * moe_amd_permute; its scratch is a static device array of
+ * MOE_PERMUTE_NOALLOC_SCRATCH_BYTES on each GPU (held until the process
+ * ends), so it accepts only S, E with moe_amd_permute_workspace_size(S, E)
+ * <= that size (e.g. E = 128 up to S of about 4.1 M routed rows) and
+ * returns MOE_ERR_UNSUPPORTED beyond.  Calls that overlap on one GPU share
+ * the array and race: order them (one stream, or events). */
+enum { MOE_PERMUTE_NOALLOC_SCRATCH_BYTES = 8 << 20 };
+int moe_amd_permute_noalloc(const int64_t* topk_index, int64_t S, int E, int32_t* counts,
+                            int32_t* offsets, int32_t* row_src, int32_t* slot, void* tile_plan,
+                            size_t tile_plan_bytes, void* stream);
+
 /* ------------------------------------------------------- grouped GEMMs */
 /* All GEMMs: bf16 operands (dtype = MOE_DTYPE_BF16), fp32 accumulation,
  * bf16 results; H and I must be multiples of 64; pointers 16-byte aligned.

@@ -51,6 +51,7 @@ SIGNATURES: dict[str, tuple] = {
     "moe_amd_permute_workspace_size": (_sz, [_i64, _i]),
     "moe_amd_tile_plan_size": (_sz, [_i64, _i]),
     "moe_amd_permute": (_i, [_p, _i64, _i, _p, _sz, _p, _p, _p, _p, _p, _sz, _p]),
+    "moe_amd_permute_noalloc": (_i, [_p, _i64, _i, _p, _p, _p, _p, _p, _sz, _p]),
     "moe_amd_gemm_gate_up_swiglu": (
         _i, [_p, _p, _i, _p, _p, _p, _i64, _i64, _i, _i, _i, _i, _p, _p, _p]),
     "moe_amd_gemm_down": (_i, [_p, _p, _p, _p, _i64, _i, _i, _i, _i, _p, _p]),

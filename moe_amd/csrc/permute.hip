@@ -13,6 +13,8 @@
 //                  lower peers, and a per-wave LDS counter carries the rank
 //                  across rounds -> stable order.
 // Ids outside [0,E) land in bin E (sentinels), after every real expert.
+#include <atomic>
+
 #include "common.h"
 
 namespace moe {
@@ -291,23 +293,28 @@ extern "C" size_t moe_amd_tile_plan_size(int64_t S, int E) {
   return plan_bytes(S, E);
 }
 
-extern "C" int moe_amd_permute(const int64_t* topk_index, int64_t S, int E, void* workspace,
-                               size_t workspace_bytes, int32_t* counts, int32_t* offsets,
-                               int32_t* row_src, int32_t* slot, void* tile_plan,
-                               size_t tile_plan_bytes, void* stream) {
-  MOE_REQUIRE(S >= 0 && S < (int64_t)1 << 31, MOE_ERR_ARG, "permute: S=%lld out of range",
+namespace moe {
+namespace {
+
+// The permutation proper: validation, then the five kernels on `stream`,
+// with `workspace` as the histogram / scan scratch.
+int permute_run(const int64_t* topk_index, int64_t S, int E, void* workspace,
+                size_t workspace_bytes, int32_t* counts, int32_t* offsets, int32_t* row_src,
+                int32_t* slot, void* tile_plan, size_t tile_plan_bytes, void* stream,
+                const char* who) {
+  MOE_REQUIRE(S >= 0 && S < (int64_t)1 << 31, MOE_ERR_ARG, "%s: S=%lld out of range", who,
               (long long)S);
-  MOE_REQUIRE(E >= 1 && E <= 16384, MOE_ERR_ARG, "permute: E=%d out of range", E);
-  MOE_REQUIRE(counts && offsets && tile_plan, MOE_ERR_ARG, "permute: null output");
+  MOE_REQUIRE(E >= 1 && E <= 16384, MOE_ERR_ARG, "%s: E=%d out of range", who, E);
+  MOE_REQUIRE(counts && offsets && tile_plan, MOE_ERR_ARG, "%s: null output", who);
   MOE_REQUIRE(tile_plan_bytes >= plan_bytes(S, E) && ((uintptr_t)tile_plan & 15) == 0,
-              MOE_ERR_WORKSPACE, "permute: tile plan needs %zu bytes, 16-byte aligned",
+              MOE_ERR_WORKSPACE, "%s: tile plan needs %zu bytes, 16-byte aligned", who,
               plan_bytes(S, E));
-  MOE_REQUIRE(S == 0 || (topk_index && row_src && slot), MOE_ERR_ARG, "permute: null pointer");
+  MOE_REQUIRE(S == 0 || (topk_index && row_src && slot), MOE_ERR_ARG, "%s: null pointer", who);
   const size_t need = permute_ws_bytes(S, E);
   MOE_REQUIRE(workspace && workspace_bytes >= need, MOE_ERR_WORKSPACE,
-              "permute: workspace %zu bytes < %zu needed", workspace_bytes, need);
+              "%s: workspace %zu bytes < %zu needed", who, workspace_bytes, need);
   const size_t lds = (size_t)kWaves * (E + 1) * sizeof(int);
-  MOE_REQUIRE(lds <= 160 * 1024, MOE_ERR_ARG, "permute: E=%d needs too much LDS", E);
+  MOE_REQUIRE(lds <= 160 * 1024, MOE_ERR_ARG, "%s: E=%d needs too much LDS", who, E);
   hipStream_t st = (hipStream_t)stream;
   const int64_t nch = (S + kChunk - 1) / kChunk;
   int* chunk_hist = (int*)workspace;
@@ -332,5 +339,71 @@ extern "C" int moe_amd_permute(const int64_t* topk_index, int64_t S, int E, void
     scatter_kernel<<<blocks, 64 * kWaves, lds, st>>>(topk_index, S, E, nch, chunk_hist,
                                                      offsets, row_src, slot);
   }
-  return check_launch("permute");
+  return check_launch(who);
+}
+
+}  // namespace
+}  // namespace moe
+
+extern "C" int moe_amd_permute(const int64_t* topk_index, int64_t S, int E, void* workspace,
+                               size_t workspace_bytes, int32_t* counts, int32_t* offsets,
+                               int32_t* row_src, int32_t* slot, void* tile_plan,
+                               size_t tile_plan_bytes, void* stream) {
+  return permute_run(topk_index, S, E, workspace, workspace_bytes, counts, offsets, row_src,
+                     slot, tile_plan, tile_plan_bytes, stream, "permute");
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free variant.  Its scratch is this file-scope device array (one
+// copy per GPU, in the code object's global segment, held until the process
+// ends).  In host code `scratch` names a host-side stand-in, not a device
+// address: the device address of each GPU's copy comes from
+// hipGetSymbolAddress, taken once per device (with that device current) on
+// the entry point's first call there, and only that address is passed to the
+// kernels.  The permutation's scratch is fully rewritten by every call (the
+// per-chunk histograms by hist_kernel, the totals by chunk_scan_kernel), so
+// nothing in it has to start at zero; calls that overlap on one GPU share the
+// array and race.
+static __device__ __align__(256) char scratch[MOE_PERMUTE_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+std::atomic<void*> g_scratch_dev[64];  // device address of `scratch`, per device
+
+int scratch_address(void** out, const char* who) {
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  MOE_REQUIRE(err == hipSuccess, MOE_ERR_HIP, "%s: hipGetDevice failed: %s", who,
+              hipGetErrorString(err));
+  MOE_REQUIRE(dev >= 0 && dev < 64, MOE_ERR_UNSUPPORTED, "%s: device %d out of range", who, dev);
+  void* p = g_scratch_dev[dev].load(std::memory_order_acquire);
+  if (!p) {
+    err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    MOE_REQUIRE(err == hipSuccess && p, MOE_ERR_HIP, "%s: hipGetSymbolAddress failed: %s", who,
+                hipGetErrorString(err));
+    g_scratch_dev[dev].store(p, std::memory_order_release);
+  }
+  *out = p;
+  return MOE_OK;
+}
+
+}  // namespace
+
+extern "C" int moe_amd_permute_noalloc(const int64_t* topk_index, int64_t S, int E,
+                                       int32_t* counts, int32_t* offsets, int32_t* row_src,
+                                       int32_t* slot, void* tile_plan, size_t tile_plan_bytes,
+                                       void* stream) {
+  const char* who = "permute_noalloc";
+  MOE_REQUIRE(S >= 0 && S < (int64_t)1 << 31 && E >= 1 && E <= 16384, MOE_ERR_ARG,
+              "%s: S=%lld or E=%d out of range", who, (long long)S, E);
+  const size_t need = permute_ws_bytes(S, E);
+  MOE_REQUIRE(need <= (size_t)MOE_PERMUTE_NOALLOC_SCRATCH_BYTES, MOE_ERR_UNSUPPORTED,
+              "%s: S=%lld, E=%d need %zu bytes of scratch, more than the %d-byte static array "
+              "(use moe_amd_permute with a workspace)", who, (long long)S, E, need,
+              MOE_PERMUTE_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  int rc = scratch_address(&ws, who);
+  if (rc) return rc;
+  return permute_run(topk_index, S, E, ws, MOE_PERMUTE_NOALLOC_SCRATCH_BYTES, counts, offsets,
+                     row_src, slot, tile_plan, tile_plan_bytes, stream, who);
 }
