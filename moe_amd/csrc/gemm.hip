@@ -351,13 +351,18 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
   uint32_t coff[CPW];  // byte offsets of this lane's column blocks at stage 0
   uint32_t roff[RPW];
   uint32_t cstep = 0, rstep = 0;  // byte advance per stage
-  auto stage_rsrc = [&](const char* ptr, uint32_t bytes, uint32_t adv) {
+  int kb_cur = 0, ke_cur = 0, nk_cur = 0;
+  // Descriptor of stage s of an operand.  Stages past the tile's last one
+  // are still issued (the wait counts count them) but get an empty extent:
+  // their loads return zeros without a memory access, so they add no L2 or
+  // HBM traffic and land quickly.
+  auto stage_rsrc = [&](const char* ptr, uint32_t bytes, uint32_t adv, int s) {
     // readfirstlane: keep the descriptor scalar (a vector descriptor would
     // turn every DMA into a waterfall loop).
-    const uint32_t left = __builtin_amdgcn_readfirstlane(adv < bytes ? bytes - adv : 0u);
+    const uint32_t left =
+        __builtin_amdgcn_readfirstlane((s < nk_cur && adv < bytes) ? bytes - adv : 0u);
     return make_rsrc(ptr + adv, left);
   };
-  int kb_cur = 0, ke_cur = 0;
   // RLT: each tile walks its k-stages starting at stage ct % nk (wrapping),
   // so that the workgroups, all starting together, read different 128-byte
   // column blocks of their token rows instead of the same block of every
@@ -380,6 +385,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
   auto setup = [&](const Tile& d) {
     kb_cur = d.kbeg;
     ke_cur = d.kend;
+    nk_cur = d.nk;
     if constexpr (MODE == RLT) {
       knk = d.nk > 0 ? d.nk : 1;
       krot = __builtin_amdgcn_readfirstlane(d.ct % knk);
@@ -526,14 +532,14 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
   };
   auto issue_col = [&](int s, const int (&tk)[NTOK > 0 ? NTOK : 1]) {
     char* base = slot_ptr(2 * s);
-    const auto rs = stage_rsrc(cptr, cbytes, kst(s) * cstep);
+    const auto rs = stage_rsrc(cptr, cbytes, kst(s) * cstep, s);
 #pragma unroll
     for (int i = 0; i < CPW; ++i) dma16(rs, col_off(s, i, tk), base + (wid + NW * i) * 1024);
   };
   // DMA of the row half of stage s (ring position 2s+1).
   auto issue_row = [&](int s) {
     char* base = slot_ptr(2 * s + 1);
-    const auto rs = stage_rsrc(rptr, rbytes, kst(s) * rstep);
+    const auto rs = stage_rsrc(rptr, rbytes, kst(s) * rstep, s);
 #pragma unroll
     for (int i = 0; i < RPW; ++i) dma16(rs, roff[i], base + (wid + NW * i) * 1024);
   };
@@ -627,8 +633,8 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
     // order, spread over 16 MFMA groups (the last sub-step of stage s-1 and
     // the first three of stage s): issued in one burst they back up the
     // texture pipe and stall MFMA issue.  Stages past the last one are
-    // still issued (their loads read zeros or in-bounds bytes that are
-    // never used) to keep the wait counts exact.
+    // still issued, with empty descriptors (zeros, no memory access), to
+    // keep the wait counts exact.
     if (cur.nk > 0) {
       int tk_a[NTOK > 0 ? NTOK : 1], tk_b[NTOK > 0 ? NTOK : 1], tn[NTOK > 0 ? NTOK : 1];
       // The wait counts rely on issue order; sched_barrier keeps the
@@ -658,11 +664,11 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
                 isrc, (uint32_t)(kb_cur + (w + 3) * BK + lane) * 4, 0, 0);
         } else if (o < NTOK + RPW) {
           const int i = o - NTOK;
-          const auto rs = stage_rsrc(rptr, rbytes, kst(w + 1) * rstep);
+          const auto rs = stage_rsrc(rptr, rbytes, kst(w + 1) * rstep, w + 1);
           dma16(rs, roff[i], slot_ptr(2 * w + 3) + (wid + NW * i) * 1024);
         } else {
           const int i = o - NTOK - RPW;
-          const auto rs = stage_rsrc(cptr, cbytes, kst(w + 2) * cstep);
+          const auto rs = stage_rsrc(cptr, cbytes, kst(w + 2) * cstep, w + 2);
           dma16(rs, col_off(w + 2, i, tk), slot_ptr(2 * w + 4) + (wid + NW * i) * 1024);
         }
       };
