@@ -230,6 +230,11 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
   constexpr int NOPS = NTOK + RPW + CPW;                  // memory ops per main-loop step
   constexpr int NGRP = (BK / 16) * TI;                    // MFMA groups per step
   static_assert(CPW * NW == 32 && RPW * NW * 8 == BR && TJ >= 1, "DMA blocks per wave");
+  // PF: the next tile's first stages are issued before this tile's epilogue,
+  // which is wave-local and issues exactly NST stores per wave.
+  constexpr bool PF = MODE == G1F || MODE == G2F || MODE == G1DX || MODE == G1DW || MODE == G2DWG;
+  constexpr int NST = (MODE == G1F ? 12 : 8) * TJ;
+  static_assert(!PF || CPW + NST <= 63, "vmcnt range");
   static_assert(TOKEN || DENSE || BR == 256, "dW modes use 256-row tiles");
 
   extern __shared__ __attribute__((aligned(16))) bf16 smem[];
@@ -609,34 +614,12 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
     else return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   };
 
-  for (; dyn ? t >= 0 : t < t_end; t = dyn ? claim() : t + nslot) {
-    const Tile cur = decode(t);
-    setup(cur);
-#pragma unroll
-    for (int i = 0; i < TI; ++i)
-#pragma unroll
-      for (int j = 0; j < TJ; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-
-    // --------------------------------------------------------- main loop
-    // Ring position h holds the column half (h = 2s) or the row half
-    // (h = 2s+1) of stage s, in slot h % 5.  Barrier B(s) comes after each
-    // wave has waited until only the last-issued column half (stage s+1)
-    // may still be in flight: stage s has landed everywhere, and every wave
-    // has finished reading stage s-1.  B(s+1) sits before the last k
-    // sub-step of stage s (whose fragments are already in registers), so
-    // that the first fragments of stage s+1 are read while those MFMAs run.
-    // Window W(s), the memory ops issued after B(s), is: the row_src
-    // entries of stage s+3 (G1DW), the DMA of the row half of stage s+1 and
-    // of the column half of stage s+2 (into stage s-1's slots), in this
-    // order, spread over 16 MFMA groups (the last sub-step of stage s-1 and
-    // the first three of stage s): issued in one burst they back up the
-    // texture pipe and stall MFMA issue.  Stages past the last one are
-    // still issued, with empty descriptors (zeros, no memory access), to
-    // keep the wait counts exact.
-    if (cur.nk > 0) {
-      int tk_a[NTOK > 0 ? NTOK : 1], tk_b[NTOK > 0 ? NTOK : 1], tn[NTOK > 0 ? NTOK : 1];
+  // The main loop's row_src entries (G1DW, G2DWG), shared by the prologue
+  // and the loop.
+  int tk_a[NTOK > 0 ? NTOK : 1], tk_b[NTOK > 0 ? NTOK : 1], tn[NTOK > 0 ? NTOK : 1];
+  // Prologue: the DMA of stage 0 and of stage 1's column half (ring
+  // positions 0, 1, 2 = slots 0, 1, 2) of the tile that setup() prepared.
+  auto prologue = [&]() {
       // The wait counts rely on issue order; sched_barrier keeps the
       // scheduler from interleaving the groups.
       fetch_tok(0, tk_a);
@@ -656,6 +639,11 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
           erow_wraw = p.rw_bf16 ? (uint32_t)((const uint16_t*)p.rw)[erow_src]
                                 : ((const uint32_t*)p.rw)[erow_src];
       }
+  };
+  // Main loop of tile `cur` (its prologue issued).  after_epi: the previous
+  // tile's epilogue stores were issued after this tile's prologue (PF modes).
+  auto mainloop = [&](const Tile& cur, bool after_epi) {
+    (void)after_epi;
       // Op o of window W(w); `tk` holds the row_src entries of stage w+2.
       auto win_op = [&](int w, int o, const int (&tk)[NTOK > 0 ? NTOK : 1]) {
         if (o < NTOK) {
@@ -684,7 +672,14 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       };
       constexpr int GQ = BK / 16 - 1;  // groups before the last sub-step: NGRP - TI
       bf16x8 fa[2][TI], fb[2][TJ];
-      WAIT_VMCNT_LGKM0(CPW);
+      if constexpr (PF) {
+        // the previous tile's NST epilogue stores were issued after this
+        // tile's first stages: they may still be in flight
+        if (after_epi) WAIT_VMCNT_LGKM0(CPW + NST);
+        else WAIT_VMCNT_LGKM0(CPW);
+      } else {
+        WAIT_VMCNT_LGKM0(CPW);
+      }
       __builtin_amdgcn_s_barrier();  // B(0)
       slot_bases(0, (uint32_t)SLOT);
 #pragma unroll
@@ -743,6 +738,204 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
           __builtin_amdgcn_sched_barrier(0);
         }
       }
+  };
+
+  // Wave-local epilogue of the PF modes.  The next tile's first stages are
+  // already in flight into ring slots 0-2; each wave writes its own
+  // WR x 128 block of the finished tile through a private 16 KB region of
+  // slots 3-4 (64 rows of 256 bytes at a time, 16-byte chunks XOR-swizzled
+  // by row so that the accumulator-layout writes spread over the banks),
+  // reads it back in row order and stores whole 256-byte row pieces, 16
+  // bytes per lane.  No workgroup barrier; every store is issued
+  // unconditionally (rows and columns outside the output get an offset past
+  // the descriptor's extent), so the next tile's first wait can leave
+  // exactly these NST stores in flight.
+  auto epilogue_pf = [&](const Tile& c) {
+    // lane- and wave-derived addresses formed here (opaque to the
+    // optimizer, which would otherwise hoist them out of the tile loop)
+    int ln = lane, wd = wid;
+    asm volatile("" : "+v"(ln), "+s"(wd));
+    const int el32 = ln & 31, ehl = ln >> 5, ewr = wd >> 1, ewc = wd & 1;
+    lds_char_t* const reg = (lds_char_t*)smem + 3 * SLOT + wd * 16384;
+    auto st16 = [&](__amdgpu_buffer_rsrc_t rs, uint32_t off, const u32x4& v) {
+      __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, 2);  // non-temporal
+    };
+    // write accumulator rows j0..j0+nj-1 of this wave into the region
+    auto write_rows = [&](int j0, int nj) {
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        if (jj >= nj) break;
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const u32x2 v = {pack_bf2(acc[i][j0 + jj][4 * q + 0], acc[i][j0 + jj][4 * q + 1]),
+                             pack_bf2(acc[i][j0 + jj][4 * q + 2], acc[i][j0 + jj][4 * q + 3])};
+            uint32_t a;
+            if constexpr (SWAP) {
+              // [output row o = tile column][64 output columns = tile rows]
+              const int o = i * 32 + el32;
+              const int ch = 4 * jj + q;
+              a = (uint32_t)o * 128 + ((uint32_t)(ch ^ ((o >> 1) & 7)) << 4) + ehl * 8;
+            } else {
+              const int r = jj * 32 + el32;
+              const int ch = 4 * i + q;
+              a = (uint32_t)r * 256 + ((uint32_t)(ch ^ (r & 15)) << 4) + ehl * 8;
+            }
+            *(__attribute__((address_space(3))) u32x2*)(reg + a) = v;
+          }
+      }
+    };
+    if constexpr (MODE == G1F) {
+      // tile columns of this wave: [gate 64 | up 64] of features fb..fb+63
+      const int fb = c.ct * 128 + ewc * 64;
+      const int r0 = c.row0 + ewr * WR;
+      const int nr = min(WR, c.row_end - r0);
+      const uint32_t rows = nr > 0 ? (uint32_t)nr : 0u;
+      const auto ra = make_rsrc(p.out + (int64_t)r0 * I, rows * (uint32_t)I * 2);
+      const auto rg = make_rsrc(p.out2 ? p.out2 + (int64_t)r0 * I2 : p.out,
+                                p.out2 ? rows * (uint32_t)I2 * 2 : 0u);
+#pragma unroll
+      for (int j0 = 0; j0 < TJ; j0 += 2) {
+        const int nj = TJ - j0 >= 2 ? 2 : 1;
+        write_rows(j0, nj);
+#pragma unroll
+        for (int it = 0; it < 4 * nj; ++it) {
+          const int rr = it * 8 + (ln >> 3), f8 = ln & 7;
+          const u32x4 gv = *(const __attribute__((address_space(3))) u32x4*)(
+              reg + rr * 256 + ((f8 ^ (rr & 15)) << 4));
+          const u32x4 uv = *(const __attribute__((address_space(3))) u32x4*)(
+              reg + rr * 256 + (((8 + f8) ^ (rr & 15)) << 4));
+          u32x4 av;
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const float g0 = bf_lo(gv[w]), g1 = bf_hi(gv[w]);
+            const float u0 = bf_lo(uv[w]), u1 = bf_hi(uv[w]);
+            av[w] = pack_bf2(round_bf(g0 * fast_sigmoid(g0)) * u0, round_bf(g1 * fast_sigmoid(g1)) * u1);
+          }
+          const int feat = fb + f8 * 8, gr = j0 * 32 + rr;
+          const bool ok = feat < I;
+          st16(ra, ok ? (uint32_t)gr * I * 2 + (uint32_t)feat * 2 : kOOB, av);
+          st16(rg, ok ? (uint32_t)gr * I2 * 2 + (uint32_t)feat * 2 : kOOB, gv);
+          st16(rg, ok ? (uint32_t)gr * I2 * 2 + (uint32_t)(I + feat) * 2 : kOOB, uv);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else if constexpr (SWAP) {
+      // G2DWG: output d_down_proj[e] [H][I]; output row = tile column,
+      // output column = tile row
+      const int o0 = c.ct * BC + ewc * 128;
+      const int no = min(128, H - o0);
+      const auto rs = make_rsrc(p.out + (int64_t)c.e * H * I + (int64_t)o0 * I,
+                                no > 0 ? (uint32_t)no * (uint32_t)I * 2 : 0u);
+#pragma unroll
+      for (int j0 = 0; j0 < TJ; j0 += 2) {
+        const int nj = TJ - j0 >= 2 ? 2 : 1;
+        write_rows(j0, nj);
+#pragma unroll
+        for (int it = 0; it < 16; ++it) {
+          const int o = it * 8 + (ln >> 3), P = ln & 7;
+          const u32x4 v = *(const __attribute__((address_space(3))) u32x4*)(reg + o * 128 + P * 16);
+          const int col = c.row0 + ewr * WR + j0 * 32 + (P ^ ((o >> 1) & 7)) * 8;
+          st16(rs, col < I ? (uint32_t)o * I * 2 + (uint32_t)col * 2 : kOOB, v);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+      // y (G2F), d_xs (G1DX): routed rows x H; d_gate_up_proj[e] (G1DW): 2I x H
+      int r0, nrows_all;
+      const bf16* ob;
+      if constexpr (TOKEN) {
+        r0 = c.row0 + ewr * WR;
+        nrows_all = c.row_end;
+        ob = p.out;
+      } else {
+        r0 = c.row0 + ewr * WR;
+        nrows_all = I2;
+        ob = p.out + (int64_t)c.e * I2 * H;
+      }
+      const int nr = min(WR, nrows_all - r0);
+      const auto rs = make_rsrc(ob + (int64_t)r0 * H, nr > 0 ? (uint32_t)nr * (uint32_t)H * 2 : 0u);
+      const int cb = c.ct * BC + ewc * 128;
+#pragma unroll
+      for (int j0 = 0; j0 < TJ; j0 += 2) {
+        const int nj = TJ - j0 >= 2 ? 2 : 1;
+        write_rows(j0, nj);
+#pragma unroll
+        for (int it = 0; it < 8 * nj; ++it) {
+          const int rr = it * 4 + (ln >> 4), P = ln & 15;
+          const u32x4 v = *(const __attribute__((address_space(3))) u32x4*)(reg + rr * 256 + P * 16);
+          const int col = cb + (P ^ (rr & 15)) * 8, gr = j0 * 32 + rr;
+          st16(rs, col < H ? (uint32_t)gr * H * 2 + (uint32_t)col * 2 : kOOB, v);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  };
+  if constexpr (PF) {
+    // (a dynamic walk may find no tile at all; every workgroup still
+    // reaches the finished-count update below)
+    Tile cur = decode(dyn ? max(t, 0) : t);
+    if (dyn ? t >= 0 : t < t_end) setup(cur);
+    if ((dyn ? t >= 0 : t < t_end) && cur.nk > 0) prologue();
+    bool first = true;
+    while (dyn ? t >= 0 : t < t_end) {
+#pragma unroll
+      for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+      if (cur.nk > 0) mainloop(cur, !first);
+      // The ring is idle: the stages past the last one have landed (empty
+      // descriptors) and every wave has finished its LDS reads.
+      WAIT_VMCNT_LGKM0(0);
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      const int tn_next = dyn ? claim() : t + nslot;
+      const bool more = dyn ? tn_next >= 0 : tn_next < t_end;
+      Tile nxt = cur;
+      if (more) {
+        nxt = decode(tn_next);
+        setup(nxt);
+        if (nxt.nk > 0) prologue();
+      }
+      epilogue_pf(cur);
+      if (!more) break;
+      cur = nxt;
+      t = tn_next;
+      first = false;
+    }
+  } else {
+  for (; dyn ? t >= 0 : t < t_end; t = dyn ? claim() : t + nslot) {
+    const Tile cur = decode(t);
+    setup(cur);
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+      for (int j = 0; j < TJ; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    // --------------------------------------------------------- main loop
+    // Ring position h holds the column half (h = 2s) or the row half
+    // (h = 2s+1) of stage s, in slot h % 5.  Barrier B(s) comes after each
+    // wave has waited until only the last-issued column half (stage s+1)
+    // may still be in flight: stage s has landed everywhere, and every wave
+    // has finished reading stage s-1.  B(s+1) sits before the last k
+    // sub-step of stage s (whose fragments are already in registers), so
+    // that the first fragments of stage s+1 are read while those MFMAs run.
+    // Window W(s), the memory ops issued after B(s), is: the row_src
+    // entries of stage s+3 (G1DW), the DMA of the row half of stage s+1 and
+    // of the column half of stage s+2 (into stage s-1's slots), in this
+    // order, spread over 16 MFMA groups (the last sub-step of stage s-1 and
+    // the first three of stage s): issued in one burst they back up the
+    // texture pipe and stall MFMA issue.  Stages past the last one are
+    // still issued, with empty descriptors (zeros, no memory access), to
+    // keep the wait counts exact.
+    if (cur.nk > 0) {
+      prologue();
+      mainloop(cur, false);
     }
 
     // --------------------------------------------------------- epilogue
@@ -998,6 +1191,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       }
     }
     __syncthreads();  // staging reads done before the next tile's stages land
+  }
   }
   if (dyn && tid == 0) {
     // The last workgroup to finish resets the counters for the next launch.
