@@ -66,6 +66,22 @@ const char* moe_amd_last_error(void);
 int moe_amd_router_linear(const void* hidden_states, const void* weight, int64_t T, int E, int H,
                           void* logits, int logits_dtype, void* stream);
 
+/* The gating linear with the softmax router fused into its epilogue:
+ * probs[T,E] fp32, topk_weights[T,K] fp32 and topk_index[T,K] int64 exactly
+ * as moe_amd_router_linear (bf16 logits) followed by
+ * moe_amd_router_softmax_topk (same logits, same top-K arithmetic, bit for
+ * bit), without the logits' round trip through memory; the bf16 logits are
+ * also written when `logits` is not NULL.  Replaces F.linear + softmax +
+ * topk + renormalisation of Qwen3MoeTopKRouter.forward
+ * (src/models/modeling_qwen3_moe.py:268-274); logit_offset [E] (may be
+ * NULL) is added before the softmax.  Shapes: H multiple of 64, E of 8,
+ * and 64 < E <= 128 with K <= 8 or 128 < E <= 256 with K <= 16 (else
+ * MOE_ERR_UNSUPPORTED). */
+int moe_amd_router_linear_softmax_topk(const void* hidden_states, const void* weight, int64_t T,
+                                       int E, int H, const float* logit_offset, int K,
+                                       int renormalize, float* probs, float* topk_weights,
+                                       int64_t* topk_index, void* logits, void* stream);
+
 /* The gating linear's input gradient for bf16 logits: d_x[T,H] =
  * bf16(d_logits[T,E] . weight[E,H]) (bf16 inputs, fp32 accumulation) -- the
  * grad_input of F.linear's backward (autograd of

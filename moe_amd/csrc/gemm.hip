@@ -60,6 +60,7 @@
 
 #include "common.h"
 #include "gemm_f32.h"
+#include "router_group.h"
 
 namespace moe {
 namespace {
@@ -78,6 +79,8 @@ constexpr int SROW = 260;  // bf16 per row of the epilogue staging tile (520 B: 
 
 // RL: the router's dense linear, logits[T, E] = x[T, H] . W_r[E, H]^T.
 // RDX: its input gradient, d_x[T, H] = d_logits[T, E] . W_r[E, H].
+// RLTK: RLT with the softmax router fused into its epilogue (probs, top-K
+//      weights and ids written from the bf16 logits of the staging tile).
 // RLT: the same logits computed transposed, rows = experts (W_r, at most one
 //      or two row tiles) and columns = tokens, with the MFMA operands
 //      swapped so that the tile is stored as logits[T, E]: for E <= 128 a
@@ -91,7 +94,7 @@ constexpr int SROW = 260;  // bf16 per row of the epilogue staging tile (520 B: 
 // computes d_down_proj[e]^T = (w act)^T d_out[tokens] and stores it
 // transposed.
 enum Mode { G1F = 0, G2F = 1, G2DX = 2, G1DX = 3, G2DW = 4, G1DW = 5, RL = 6, RDX = 7, RDW = 8,
-            G2DXF = 9, G2DWG = 10, RLT = 11 };
+            G2DXF = 9, G2DWG = 10, RLT = 11, RLTK = 12 };
 
 struct GemmArgs {
   const bf16* x;         // hidden_states [T,H]
@@ -114,6 +117,11 @@ struct GemmArgs {
   uint32_t tok_mul;      // n / topk == (n * tok_mul) >> tok_shift for 0 <= n < 2^31
   int tok_shift;         // 31 + ceil(log2(topk))
   int n_ct, n_rt, n_tiles;  // n_tiles: dW modes (host-known)
+  float* probs;          // RLTK: router outputs probs [T,E] fp32, top-K weights [T,K] fp32,
+  float* topk_w;         //   top-K ids [T,K] int64; logit offset [E] (may be null)
+  int64_t* topk_idx;
+  const float* offset;
+  int renorm;
   int* queue;            // G2DW/G1DW: this GEMM's 8 XCD tile counters + finished count (null: static walk)
   const int* xstart;     // ... experts of XCD x: xorder[xstart[x] .. xstart[x+1])
   const int* xorder;
@@ -213,14 +221,15 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
   constexpr int NW = kWaves<BR>;                          // waves, as NW/2 rows x 2 columns
   constexpr int NTHR = NW * 64;
   constexpr bool TOKEN = MODE <= G1DX || MODE == G2DXF;   // rows = routed rows of one expert
-  constexpr bool DENSE = MODE == RL || MODE == RDX || MODE == RLT;  // one "expert", dense rows
-  constexpr bool COL_KM = !(MODE == G1F || MODE == G2F || MODE == RL || MODE == RLT);  // k-major cols
+  constexpr bool TRL = MODE == RLT || MODE == RLTK;        // transposed router linear
+  constexpr bool DENSE = MODE == RL || MODE == RDX || TRL;  // one "expert", dense rows
+  constexpr bool COL_KM = !(MODE == G1F || MODE == G2F || MODE == RL || TRL);  // k-major cols
   constexpr bool ROW_KM = !TOKEN && !DENSE;               // row operand k-major (dW)
   constexpr bool DOWN_DX = MODE == G2DX || MODE == G2DXF;  // column operand down_proj[e], k-major
   constexpr bool GROW = MODE == G1F || MODE == G2DXF;      // row operand: token rows via row_src
   constexpr bool GCOL = MODE == G1DW || MODE == G2DWG;     // column operand: token rows via row_src (k-major)
   constexpr bool DW = MODE == G2DW || MODE == G1DW || MODE == G2DWG;
-  constexpr bool SWAP = MODE == G2DWG || MODE == RLT;  // MFMA operands swapped: lanes hold 4 consecutive rows
+  constexpr bool SWAP = MODE == G2DWG || TRL;  // MFMA operands swapped: lanes hold 4 consecutive rows
   constexpr int WR = BR / (NW / 2);                       // rows per wave
   constexpr int TJ = WR / 32;                             // MFMA row sub-tiles per wave
   constexpr int TI = 4;                                   // MFMA col sub-tiles per wave (128 cols)
@@ -299,7 +308,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       d.ct = tt % p.n_ct;
       d.e = 0;
       d.row0 = (tt / p.n_ct) * BR;
-      d.row_end = (int)min((int64_t)d.row0 + BR, MODE == RLT ? (int64_t)p.E : p.T);
+      d.row_end = (int)min((int64_t)d.row0 + BR, TRL ? (int64_t)p.E : p.T);
       d.kbeg = d.kend = 0;
     } else {
       const int vi = tt / per_e;
@@ -326,7 +335,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
     d.kbeg = __builtin_amdgcn_readfirstlane(d.kbeg);
     d.kend = __builtin_amdgcn_readfirstlane(d.kend);
     int K_len;
-    if constexpr (MODE == G1F || DOWN_DX || MODE == RL || MODE == RLT) K_len = H;
+    if constexpr (MODE == G1F || DOWN_DX || MODE == RL || TRL) K_len = H;
     else if constexpr (MODE == RDX) K_len = p.E;
     else if constexpr (MODE == G2F) K_len = I;
     else if constexpr (MODE == G1DX) K_len = I2;
@@ -374,7 +383,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
   // row at once (which lands on few HBM channels).  Other modes: identity.
   int krot = 0, knk = 1;
   auto kst = [&](int st) -> uint32_t {
-    if constexpr (MODE == RLT) {
+    if constexpr (TRL) {
       int v = st + krot;
       v -= v >= knk ? knk : 0;
       v -= v >= knk ? knk : 0;
@@ -391,7 +400,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
     kb_cur = d.kbeg;
     ke_cur = d.kend;
     nk_cur = d.nk;
-    if constexpr (MODE == RLT) {
+    if constexpr (TRL) {
       knk = d.nk > 0 ? d.nk : 1;
       krot = __builtin_amdgcn_readfirstlane(d.ct % knk);
     }
@@ -408,7 +417,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
         coff[i] = (uint32_t)wrow * (uint32_t)(H * 2) + kc_chunk(f) * 16;
       }
       cstep = BK * 2;
-    } else if constexpr (MODE == RLT) {
+    } else if constexpr (TRL) {
       // hidden_states rows [T][H]: tokens are the tile's columns
       cptr = (const char*)p.x;
       cbytes = (uint32_t)(p.T * H * 2);
@@ -480,7 +489,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       }
       rstep = BK * 2;
     } else if constexpr (TOKEN || DENSE) {
-      const int ld = (MODE == G2F) ? I : ((MODE == G2DX || MODE == RL || MODE == RLT) ? H : (MODE == RDX ? p.E : I2));
+      const int ld = (MODE == G2F) ? I : ((MODE == G2DX || MODE == RL || TRL) ? H : (MODE == RDX ? p.E : I2));
       rptr = (const char*)(p.a0 + (int64_t)d.row0 * ld);
       rbytes = (uint32_t)((int64_t)(d.row_end - d.row0) * ld * 2);
 #pragma unroll
@@ -1135,6 +1144,71 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
           }
         }
       }
+    } else if constexpr (MODE == RLTK) {
+      // The softmax router fused into the gating linear.  The staging tile
+      // holds the bf16 logits of BC tokens x BR experts ([token][expert]);
+      // G lanes per token run the softmax router's top-K core
+      // (router_group.h) on them -- the arithmetic of router_linear with
+      // bf16 logits followed by router_softmax_topk, bit for bit -- and
+      // write probs, the top-K weights and ids, and (if asked) the logits.
+      constexpr int G = BR == 128 ? 8 : 16, V = 16, TPP = NTHR / G;
+      const int g = tid & (G - 1), e0 = g * V;
+      const int E = p.E, K = p.topk;
+      const bool has_off = p.offset != nullptr;
+      float off[V];
+#pragma unroll
+      for (int j = 0; j < V; ++j) off[j] = (has_off && e0 + j < E) ? p.offset[e0 + j] : 0.f;
+      for (int rr = tid / G; rr < BC; rr += TPP) {
+        const int64_t t = (int64_t)cur.ct * BC + rr;
+        const bool tok = t < p.T;
+        u32x2 raw[V / 4];
+#pragma unroll
+        for (int q = 0; q < V / 4; ++q) raw[q] = *(const u32x2*)(stg + rr * SROW + e0 + 4 * q);
+        float v[V], m, s, pr[V], my_w;
+        int my_e;
+        if (!has_off) {
+          // bf16 values: 32-bit keys (value bits and index), as the router
+          // kernel uses for bf16 logits without an offset.
+          uint32_t key[V];
+#pragma unroll
+          for (int j = 0; j < V; ++j) {
+            const int e = e0 + j;
+            const uint32_t bits = (raw[j >> 2][(j >> 1) & 1] >> (16 * (j & 1))) & 0xffffu;
+            v[j] = e < E ? __uint_as_float(bits << 16) : -INFINITY;
+            key[j] = e < E ? rank_key16(bits, e) : 0u;
+          }
+          group_softmax<G, V>(v, key, e0, E, pr, m, s);
+          group_topk<G, V>(key, m, 1.f / s, g, K, p.renorm, my_w, my_e);
+        } else {
+          uint64_t key[V];
+#pragma unroll
+          for (int j = 0; j < V; ++j) {
+            const int e = e0 + j;
+            const uint32_t bits = (raw[j >> 2][(j >> 1) & 1] >> (16 * (j & 1))) & 0xffffu;
+            v[j] = e < E ? __uint_as_float(bits << 16) + off[j] : -INFINITY;
+            key[j] = e < E ? rank_key(v[j], e) : 0ull;
+          }
+          group_softmax<G, V>(v, key, e0, E, pr, m, s);
+          group_topk<G, V>(key, m, 1.f / s, g, K, p.renorm, my_w, my_e);
+        }
+        const float rs = 1.f / s;
+        if (tok) {
+#pragma unroll
+          for (int q = 0; q < V / 4; ++q)
+            if (e0 + 4 * q < E)
+              *(f32x4*)(p.probs + t * E + e0 + 4 * q) =
+                  f32x4{pr[4 * q] * rs, pr[4 * q + 1] * rs, pr[4 * q + 2] * rs, pr[4 * q + 3] * rs};
+          if (g < K) {
+            p.topk_w[t * K + g] = my_w;
+            p.topk_idx[t * K + g] = my_e;
+          }
+          if (p.out) {
+#pragma unroll
+            for (int q = 0; q < V / 4; ++q)
+              if (e0 + 4 * q < E) *(u32x2*)(p.out + t * E + e0 + 4 * q) = raw[q];
+          }
+        }
+      }
     } else if constexpr (MODE == RLT) {
       // bf16 logits from the transposed staging: BC token rows of BR
       // experts; BR/8 lanes per row, 16 bytes each.
@@ -1159,8 +1233,8 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
         ld = H;
         obase = p.out;
       } else if constexpr (DENSE) {
-        nrows = MODE == RLT ? (int)p.T : cur.row_end;  // RLT: rows of the stored tile are tokens
-        ld = (MODE == RL || MODE == RLT) ? p.E : H;
+        nrows = TRL ? (int)p.T : cur.row_end;  // RLT: rows of the stored tile are tokens
+        ld = (MODE == RL || TRL) ? p.E : H;
         obase = p.out;
       } else {
         constexpr bool DOWN = MODE == G2DW || MODE == G2DWG;
@@ -1230,7 +1304,7 @@ int launch(const GemmArgs& a, int max_tiles, hipStream_t st) {
   constexpr size_t stages = (size_t)NSLOT * SLOT;
   // staging tile ([BC][SROW] when transposed), plus G2DXF's per-row weights
   // and row_src
-  constexpr size_t staging = (size_t)((MODE == G2DWG || MODE == RLT) ? BC : BR) * SROW * sizeof(bf16) +
+  constexpr size_t staging = (size_t)((MODE == G2DWG || MODE == RLT || MODE == RLTK) ? BC : BR) * SROW * sizeof(bf16) +
                              (MODE == G2DXF ? (size_t)BR * 8 : 0);
   const size_t lds = stages > staging ? stages : staging;
   if (max_tiles <= 0) return MOE_OK;
@@ -1404,6 +1478,52 @@ extern "C" int moe_amd_router_linear(const void* hidden_states, const void* weig
   MOE_REQUIRE(n_tiles < ((int64_t)1 << 30), MOE_ERR_UNSUPPORTED, "%s: too many tiles", who);
   a.n_tiles = (int)n_tiles;
   return launch<RL, 256>(a, a.n_tiles, (hipStream_t)stream);
+}
+
+extern "C" int moe_amd_router_linear_softmax_topk(const void* hidden_states, const void* weight,
+                                                  int64_t T, int E, int H,
+                                                  const float* logit_offset, int K,
+                                                  int renormalize, float* probs,
+                                                  float* topk_weights, int64_t* topk_index,
+                                                  void* logits, void* stream) {
+  const char* who = "router_linear_softmax_topk";
+  MOE_REQUIRE(T >= 0 && E >= 1 && H > 0 && K >= 1 && K <= E, MOE_ERR_ARG, "%s: bad sizes", who);
+  MOE_REQUIRE(H % 64 == 0 && E % 8 == 0, MOE_ERR_ARG,
+              "%s: H=%d must be a multiple of 64 and E=%d of 8", who, H, E);
+  // The fused epilogue runs the router's group top-K with 16 experts per
+  // lane: 8 lanes per token for E in (64, 128] and K <= 8, 16 lanes for E
+  // in (128, 256] and K <= 16 (the router kernel's own shapes there).
+  const bool g8 = E > 64 && E <= 128 && K <= 8, g16 = E > 128 && E <= 256 && K <= 16;
+  MOE_REQUIRE(g8 || g16, MOE_ERR_UNSUPPORTED,
+              "%s: E=%d, K=%d outside the fused shapes (64 < E <= 128 with K <= 8, 128 < E <= "
+              "256 with K <= 16); use moe_amd_router_linear + moe_amd_router_softmax_topk", who,
+              E, K);
+  MOE_REQUIRE(weight && (T == 0 || (hidden_states && probs && topk_weights && topk_index)),
+              MOE_ERR_ARG, "%s: null pointer", who);
+  MOE_ALIGNED(hidden_states, who);
+  MOE_ALIGNED(weight, who);
+  MOE_ALIGNED(probs, who);
+  MOE_REQUIRE(((uintptr_t)logits & 7) == 0, MOE_ERR_ALIGN, "%s: logits not 8-byte aligned", who);
+  MOE_REQUIRE(T * (int64_t)H * 2 < ((int64_t)1 << 31) && (int64_t)E * H * 2 < ((int64_t)1 << 31),
+              MOE_ERR_UNSUPPORTED, "%s: T*H or E*H too large for 32-bit offsets", who);
+  if (T == 0) return MOE_OK;
+  GemmArgs a{};
+  a.x = (const bf16*)hidden_states;
+  a.a0 = (const bf16*)weight;
+  a.out = (bf16*)logits;
+  a.probs = probs;
+  a.topk_w = topk_weights;
+  a.topk_idx = topk_index;
+  a.offset = logit_offset;
+  a.renorm = renormalize;
+  a.topk = K;
+  a.T = T; a.E = E; a.H = H; a.I = 64;
+  a.n_ct = (int)((T + BC - 1) / BC);
+  a.n_rt = 1;
+  MOE_REQUIRE(a.n_ct < (1 << 30), MOE_ERR_UNSUPPORTED, "%s: too many tiles", who);
+  a.n_tiles = a.n_ct;
+  if (g8) return launch<RLTK, 128>(a, a.n_tiles, (hipStream_t)stream);
+  return launch<RLTK, 256>(a, a.n_tiles, (hipStream_t)stream);
 }
 
 namespace {

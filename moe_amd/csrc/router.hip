@@ -8,6 +8,7 @@
 // Reference: src/models/modeling_qwen3_moe.py:266-275,
 //            src/models/router.py:22-70 and :103-155.
 #include "common.h"
+#include "router_group.h"
 #include "wave_topk.h"
 
 #include <cmath>
@@ -217,10 +218,11 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void sigmoid_topk_group_kernel
 // rank_key with G-lane DPP butterflies.  Per token this takes about a fifth
 // of the VALU instructions of the wave-per-token kernel, which at E = 128 is
 // VALU-bound (64-lane reductions repeated K times for 2 values per lane).
-// Same arithmetic: probs = exp(v - max) / sum with the sum over the group in
-// a fixed butterfly order; the selected weights are those probs (recomputed
-// bit-identically from the winning key), renormalised by their sum in rank
-// order.
+// probs = exp(v - max) * (1 / sum) with the sum over the group in a fixed
+// butterfly order; the selected weights are those probs (recomputed
+// bit-identically from the winning key), renormalised by their group sum.
+// The gating linear's fused epilogue (gemm.hip) runs the same core
+// (router_group.h) and writes the same bits.
 template <int G, int V, bool KEY16, bool VEC>
 __global__ __launch_bounds__(64 * kWavesPerBlock) void softmax_topk_group_kernel(
     const void* __restrict__ logits, int logits_dtype, const float* __restrict__ offset,
@@ -275,62 +277,26 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void softmax_topk_group_kernel
         }
       }
     }
-    // A NaN logit makes every prob of the row NaN, and the reference ranks
-    // the probs: the row's entries then all tie and rank by index.
-    uint32_t nan_row = 0;
-#pragma unroll
-    for (int j = 0; j < V; ++j) nan_row |= (uint32_t)(v[j] != v[j]);
-    if (group_max_key<G>(nan_row)) {
-#pragma unroll
-      for (int j = 0; j < V; ++j) {
-        const int e = e0 + j;
-        if constexpr (KEY16) key[j] = e < E ? rank_key16(0x7fc0u, e) : 0u;
-        else key[j] = e < E ? rank_key(__builtin_nanf(""), e) : 0ull;
-      }
-    }
-    float m = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < V; ++j) m = fmaxf(m, v[j]);
-    m = group_max<G>(m);
-    float p[V];
-    float s = 0.f;
-#pragma unroll
-    for (int j = 0; j < V; ++j) {
-      p[j] = (e0 + j < E) ? expf(v[j] - m) : 0.f;
-      s += p[j];
-    }
-    s = group_sum<G>(s);
+    float m, s, p[V];
+    group_softmax<G, V>(v, key, e0, E, p, m, s);
+    const float rs = 1.f / s;
     if constexpr (VEC) {
       if (tok) {
         f32x4* dst = (f32x4*)(probs + t * E + e0);
 #pragma unroll
         for (int q = 0; q < V / 4; ++q)
-          dst[q] = f32x4{p[4 * q] / s, p[4 * q + 1] / s, p[4 * q + 2] / s, p[4 * q + 3] / s};
+          dst[q] = f32x4{p[4 * q] * rs, p[4 * q + 1] * rs, p[4 * q + 2] * rs, p[4 * q + 3] * rs};
       }
     } else {
 #pragma unroll
       for (int j = 0; j < V; ++j) {
         const int e = e0 + j;
-        if (tok && e < E) probs[t * E + e] = p[j] / s;
+        if (tok && e < E) probs[t * E + e] = p[j] * rs;
       }
     }
-    float my_w = 0.f, ssum = 0.f;
-    int my_e = 0;
-    for (int k = 0; k < K; ++k) {
-      Key b = key[0];
-#pragma unroll
-      for (int j = 1; j < V; ++j) b = key[j] > b ? key[j] : b;
-      b = group_max_key<G>(b);
-#pragma unroll
-      for (int j = 0; j < V; ++j) key[j] = key[j] == b ? 0 : key[j];
-      const float pe = expf(key_value(b) - m) / s;  // == probs of the winner
-      ssum += pe;
-      if (g == k) {
-        my_w = pe;
-        my_e = key_index(b);
-      }
-    }
-    if (renorm) my_w = my_w / ssum;
+    float my_w;
+    int my_e;
+    group_topk<G, V>(key, m, rs, g, K, renorm, my_w, my_e);
     if (tok && g < K) {
       topk_w[t * K + g] = my_w;
       topk_idx[t * K + g] = my_e;

@@ -8,7 +8,10 @@ call the reference makes, so the logits and therefore the routing are the
 reference's, bit for bit) or the MFMA kernel (``gating="hip"``: the same
 exact bf16 products summed in the kernel's own fp32 order, so a top-k choice
 between experts whose logits tie within one bf16 rounding can differ); its
-backward runs on the MFMA kernels either way.
+backward runs on the MFMA kernels either way.  ``gating="hip_fused"`` (softmax
+router) runs the router in the MFMA gating kernel's epilogue: the same bits as
+"hip", without the logits' round trip (shapes the fused kernel does not cover
+take the two-kernel form, with the same results).
 ``SparseMoeBlock`` wraps it with the reference's parameter names
 (``gate.weight``, ``experts.gate_up_proj``, ``experts.down_proj``).
 """
@@ -39,7 +42,7 @@ def moe_layer(x: torch.Tensor, w_router: torch.Tensor, gate_up_proj: torch.Tenso
     """Returns (out [T,H], router_logits [T,E] fp32, weights [T,K], index [T,K])."""
     if gating not in library.GATINGS:
         raise ValueError(f"unknown gating {gating!r} (expected one of {library.GATINGS})")
-    hip = gating == "hip"
+    hip = gating in ("hip", "hip_fused")
     if router == "softmax" and _fused_softmax_ok(x, w_router, gate_up_proj, down_proj):
         # Gating linear + softmax router + experts as ONE autograd node (op
         # moe_amd::moe_layer_fwd), so that the two gradients of the hidden

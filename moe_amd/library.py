@@ -366,17 +366,19 @@ torch.library.register_autograd(f"{_LIB}::sigmoid_topk", _sigmoid_backward,
 
 # ------------------------------------------------ softmax layer, one node
 
-GATINGS = ("torch", "hip")
+GATINGS = ("torch", "hip", "hip_fused")
 
 
 def gating_logits(x: Tensor, w_router: Tensor, gating: str, fp32: bool) -> Tensor:
     """Router logits from the gating source ``gating``: "torch" = the
     reference's F.linear on this device (bit-identical logits, hence the
     reference's routing), "hip" = the MFMA gating-linear kernel (same exact
-    products, its own fp32 summation order)."""
+    products, its own fp32 summation order); "hip_fused" computes the same
+    logits as "hip" (the softmax router then runs in the kernel's
+    epilogue)."""
     if gating == "torch":
         return ops.torch_gating_linear(x, w_router, fp32)
-    if gating == "hip":
+    if gating in ("hip", "hip_fused"):
         return ops.router_linear(x, w_router, torch.float32 if fp32 else torch.bfloat16)
     raise ValueError(f"unknown gating {gating!r} (expected one of {GATINGS})")
 
@@ -392,9 +394,14 @@ def moe_layer_fwd(x: Tensor, w_router: Tensor, gate_up_proj: Tensor, down_proj: 
     experts (Qwen3MoeSparseMoeBlock.forward, src/models/modeling_qwen3_moe.py:
     284-289).  The backward runs the gating linear's gradients on the MFMA
     kernels whichever source computed the logits."""
-    logits = gating_logits(x, w_router, gating, fp32=False)
-    probs, w, idx = ops.router_softmax_topk(logits, top_k, renormalize, logit_offset)
-    del logits
+    if gating == "hip_fused" and ops.router_fused_supported(w_router.shape[0], top_k):
+        # gating linear + softmax router in one kernel (same bits as "hip")
+        probs, w, idx = ops.router_linear_softmax_topk(x, w_router, top_k, renormalize,
+                                                       logit_offset)
+    else:
+        logits = gating_logits(x, w_router, gating, fp32=False)
+        probs, w, idx = ops.router_softmax_topk(logits, top_k, renormalize, logit_offset)
+        del logits
     plan = ops.permute(idx, gate_up_proj.shape[0])
     gu, act = ops.gemm_gate_up_swiglu(x, plan, gate_up_proj, save_gate_up=save_for_backward)
     y = ops.gemm_down(act, plan, down_proj)

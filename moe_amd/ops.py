@@ -106,6 +106,43 @@ def router_linear(x: torch.Tensor, weight: torch.Tensor,
     return logits
 
 
+def router_fused_supported(E: int, top_k: int) -> bool:
+    """Shapes of router_linear_softmax_topk (the router's 16-experts-per-lane
+    group shapes)."""
+    return (64 < E <= 128 and top_k <= 8) or (128 < E <= 256 and top_k <= 16)
+
+
+def router_linear_softmax_topk(x: torch.Tensor, weight: torch.Tensor, top_k: int,
+                               renormalize: bool = True,
+                               logit_offset: torch.Tensor | None = None,
+                               return_logits: bool = False):
+    """The gating linear with the softmax router fused into its epilogue:
+    (probs fp32 [T,E], weights fp32 [T,K], index int64 [T,K][, bf16 logits
+    [T,E]]), bit-identical to router_linear(x, weight, bf16) followed by
+    router_softmax_topk."""
+    _need_cuda(x, weight, logit_offset)
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise TypeError("router_linear_softmax_topk takes bf16 hidden states and weight")
+    x = _contig(x)
+    weight = _contig(weight)
+    T, H = x.shape
+    E = weight.shape[0]
+    if weight.shape[1] != H:
+        raise ValueError(f"router_linear_softmax_topk: weight {tuple(weight.shape)} vs hidden "
+                         f"{tuple(x.shape)}")
+    dev = x.device
+    probs = torch.empty(T, E, device=dev, dtype=torch.float32)
+    w = torch.empty(T, top_k, device=dev, dtype=torch.float32)
+    idx = torch.empty(T, top_k, device=dev, dtype=torch.int64)
+    logits = torch.empty(T, E, device=dev, dtype=torch.bfloat16) if return_logits else None
+    if logit_offset is not None:
+        logit_offset = _contig(logit_offset.to(torch.float32))
+    _call("moe_amd_router_linear_softmax_topk", x.data_ptr(), weight.data_ptr(), T, E, H,
+          _ptr(logit_offset), int(top_k), int(renormalize), probs.data_ptr(), w.data_ptr(),
+          idx.data_ptr(), _ptr(logits), _stream(x))
+    return (probs, w, idx, logits) if return_logits else (probs, w, idx)
+
+
 def router_linear_backward_dx(d_logits: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     """d_x [T,H] = bf16(d_logits [T,E] . weight [E,H]) on MFMA (bf16 inputs)."""
     _need_cuda(d_logits, weight)

@@ -208,7 +208,8 @@ def test_layer_routing_weight_grad_sampled():
 
 # M first: the sampled routing-weight test above drew its inputs (one
 # workload is cached at a time); Retrofit last, for the schedule test below.
-BF16_CASES = [(c, g) for c in ("m_skew", "xs_global", "l", "retrofit") for g in ("torch", "hip")]
+BF16_CASES = ([(c, g) for c in ("m_skew", "xs_global", "l", "retrofit") for g in ("torch", "hip")]
+              + [("l", "hip_fused"), ("xs_global", "hip_fused")])
 
 
 @pytest.mark.parametrize("name,gating", BF16_CASES)

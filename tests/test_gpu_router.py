@@ -263,3 +263,62 @@ def test_router_nan_rows(router, E, K, dtype):
     assert torch.equal(torch.isnan(w.cpu()).any(-1), nan_rows)
     ok = ~nan_rows
     assert torch.allclose(w.cpu()[ok], w_ref[ok], rtol=1e-5, atol=1e-7)
+
+
+@pytest.mark.parametrize("T,H,E,K,with_off", [
+    (65536, 2048, 128, 8, False),   # L / M shape, full token count
+    (16384, 1024, 128, 4, True),    # XS global bank with the logit offset
+    (1000, 256, 256, 12, True),     # 16 lanes per token, K > 8
+    (777, 128, 200, 8, False),      # 16 lanes per token, partly empty lanes, ragged T
+    (333, 192, 72, 6, True),        # 8 lanes per token, mostly empty lanes, ragged T
+    (5, 64, 136, 16, False),        # fewer tokens than one tile, K = 16
+])
+def test_router_fused_softmax_topk(T, H, E, K, with_off):
+    """The gating linear with the softmax router in its epilogue equals the
+    two-kernel form (router_linear bf16 -> router_softmax_topk) bit for bit --
+    probabilities, weights, ids and the logits it writes -- and the oracle's
+    routing on those logits exactly."""
+    print(f"fused router T={T} H={H} E={E} K={K} offset={with_off}", flush=True)
+    g = torch.Generator().manual_seed(T + E + K)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(DEV)
+    wr = (torch.randn(E, H, generator=g) * 0.05).to(torch.bfloat16).to(DEV)
+    off = ((torch.rand(E, generator=g) * 2 - 1) * 0.5).to(DEV) if with_off else None
+    for renorm in (True, False):
+        probs, w, idx, lg = ops.router_linear_softmax_topk(x, wr, K, renorm, off,
+                                                          return_logits=True)
+        logits = ops.router_linear(x, wr, torch.bfloat16)
+        p2, w2, i2 = ops.router_softmax_topk(logits, K, renorm, off)
+        p3, w3, i3 = ops.router_linear_softmax_topk(x, wr, K, renorm, off)
+        torch.cuda.synchronize()
+        assert torch.equal(lg, logits), "fused logits differ from router_linear's"
+        assert torch.equal(idx, i2) and torch.equal(i3, i2), "fused routing ids differ"
+        for a, b in ((probs, p2), (w, w2), (p3, p2), (w3, w2)):
+            assert torch.equal(a.view(torch.int32), b.view(torch.int32)), "fused values differ"
+        if T <= 20000:
+            p_ref, w_ref, i_ref = O.softmax_router(logits.cpu(), K, renorm,
+                                                   None if off is None else off.cpu())
+            assert torch.equal(idx.cpu(), i_ref)
+            assert torch.allclose(probs.cpu(), p_ref, rtol=1e-5, atol=1e-7)
+            assert torch.allclose(w.cpu(), w_ref, rtol=1e-5, atol=1e-7)
+
+
+def test_router_fused_nan_rows_and_rejects():
+    """A NaN hidden state makes its token's logits NaN: the fused router
+    routes it as the two-kernel form does (the K lowest ids); shapes outside
+    the fused kernel's are refused with the two-kernel form named."""
+    g = torch.Generator().manual_seed(5)
+    T, H, E, K = 300, 128, 128, 8
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    x[7, 3] = float("nan")
+    x, wr = x.to(DEV), (torch.randn(E, H, generator=g) * 0.05).to(torch.bfloat16).to(DEV)
+    probs, w, idx = ops.router_linear_softmax_topk(x, wr, K)
+    p2, w2, i2 = ops.router_softmax_topk(ops.router_linear(x, wr, torch.bfloat16), K)
+    torch.cuda.synchronize()
+    assert torch.equal(idx, i2) and idx[7].tolist() == list(range(K))
+    assert torch.equal(probs.view(torch.int32), p2.view(torch.int32))
+    assert torch.equal(w.view(torch.int32), w2.view(torch.int32))
+    for e, k in ((64, 4), (1792, 8), (128, 9)):
+        wbad = torch.zeros(e, H, dtype=torch.bfloat16, device=DEV)
+        with pytest.raises(RuntimeError, match="router_softmax_topk"):
+            ops.router_linear_softmax_topk(x, wbad, k)
+    assert ops.router_linear_softmax_topk(x[:0], wr, K)[2].shape == (0, K)
