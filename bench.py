@@ -55,15 +55,26 @@ def gemm_flops(name: str, S: int, H: int, I: int) -> float:
 
 
 def hbm_bytes(name: str, cfg) -> float:
-    """Algorithmic HBM bytes of the gather-shaped kernels (b = 2 for bf16)."""
-    T, H, K, E, S = cfg.T, cfg.H, cfg.K, cfg.E, cfg.S
-    b = 2
+    """Algorithmic HBM bytes of a launch: each operand read once (routed rows
+    as gathered, S*H), each output written once (b = element size)."""
+    T, H, K, E, S, I = cfg.T, cfg.H, cfg.K, cfg.E, cfg.S, cfg.I
+    b = 2 if cfg.dtype == torch.bfloat16 else 4
+    w1, w2 = E * 2 * I * H * b, E * H * I * b
     per = {
         "moe_amd_combine": S * H * b + S * 8 + T * H * b,
         "moe_amd_combine_backward": T * H * b + 2 * S * H * b + S * 12,
         "moe_amd_gather_backward": S * H * b + S * 4 + T * H * b,
         "moe_amd_gather_backward_add": S * H * b + S * 4 + 2 * T * H * b,
         "moe_amd_permute": S * 8 + S * 4 * 2 + E * 4,
+        # x rows, gate_up_proj in; gate_up and act out
+        "moe_amd_gemm_gate_up_swiglu": S * H * b + w1 + S * 2 * I * b + S * I * b,
+        "moe_amd_gemm_down": S * I * b + w2 + S * H * b,
+        # d_out rows, down_proj, gate_up, weights in; d_gate_up, act_w, partials out
+        "moe_amd_gemm_down_backward_dx_fused": S * H * b + w2 + 2 * S * 2 * I * b + S * I * b
+        + S * 3 * 4,
+        "moe_amd_gemm_down_backward_dw_gathered": S * H * b + S * I * b + w2,
+        "moe_amd_gemm_gate_up_backward_dx": S * 2 * I * b + w1 + S * H * b,
+        "moe_amd_gemm_gate_up_backward_dw": S * 2 * I * b + S * H * b + w1,
     }
     return per.get(name, 0.0)
 
@@ -363,7 +374,17 @@ def main():
     dom = max(gemms, key=lambda n: sum(gemms[n]))
     dom_avg = sum(gemms[dom]) / len(gemms[dom])
     dom_fl = gemm_flops(dom, cfg.S, cfg.H, cfg.I)
-    achieved = dom_fl / dom_avg / 1e9
+    dom_by = hbm_bytes(dom, cfg)
+    # The dominant GEMM's bound: MFMA when its arithmetic intensity
+    # (algorithmic FLOP per algorithmic HBM byte) exceeds the machine balance
+    # peak / 8 TB/s, else HBM (the 1792-expert bank's weight gradients).
+    if dom_fl / dom_by >= peak * 1e12 / (PEAK_HBM_GBS * 1e9):
+        roof = {"bound": "mfma", "achieved": round(dom_fl / dom_avg / 1e9, 1), "peak": peak,
+                "unit": "TFLOP/s"}
+    else:
+        roof = {"bound": "hbm", "achieved": round(dom_by / dom_avg / 1e6, 1),
+                "peak": PEAK_HBM_GBS, "unit": "GB/s"}
+    roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
     counts = torch.bincount(idx.reshape(-1), minlength=cfg.E)
     imbalance = counts.max().item() / (cfg.S / cfg.E)
     log(f"[bench] per-kernel pass: {args.kernel_steps} steps, {k_ms:.3f} ms/step")
@@ -393,10 +414,9 @@ def main():
                  "frac_peak": round(gemm_fl / gemm_ms / 1e9 / peak, 4),
                  "timed_in": f"separate per-kernel pass of {args.kernel_steps} steps "
                              f"({k_ms:.3f} ms/step with the events)"},
-        "roofline": {"bound": "mfma", "kernel": dom.replace("moe_amd_", ""),
-                     "achieved": round(achieved, 1), "peak": peak,
-                     "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
-                     "traffic": recorded_traffic(cfg.name, dom.replace("moe_amd_", ""))},
+        "roofline": dict(roof, kernel=dom.replace("moe_amd_", ""),
+                         algorithmic_bytes=dom_by, flops=dom_fl,
+                         traffic=recorded_traffic(cfg.name, dom.replace("moe_amd_", ""))),
         "kernels": kernels,
         "routing": dict(routing_gating_check(cfg, x, wr, inp),
                         timed_gating=args.gating,

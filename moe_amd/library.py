@@ -152,11 +152,16 @@ def _(d_out, hidden_states, top_k_weights, gate_up_proj, down_proj, gate_up, act
 def _experts_setup(ctx, inputs, output):
     x, _, w, w1, w2, _ = inputs
     _, gu, act, y, counts, offsets, row_src, slot, tile_plan = output
+    # The saved activations are outputs only for saving: no zero [S, 2I]
+    # gradient is materialised for them.
+    ctx.set_materialize_grads(False)
     ctx.save_for_backward(x, w, w1, w2, gu, act, y, counts, offsets, row_src, slot, tile_plan)
 
 
 def _experts_backward(ctx, d_out, *unused):
     need_x, _, need_w, need_w1, need_w2 = ctx.needs_input_grad[:5]
+    if d_out is None:
+        return (None,) * 6
     d_x, d_w, d_w1, d_w2 = torch.ops.moe_amd.experts_bwd(
         d_out, *ctx.saved_tensors, bool(need_x), bool(need_w1), bool(need_w2))
     return (d_x if need_x else None, None, d_w if need_w else None, d_w1 if need_w1 else None,
@@ -234,6 +239,32 @@ def _linear_backward(ctx, d_logits):
 
 torch.library.register_autograd(f"{_LIB}::router_linear", _linear_backward,
                                 setup_context=_linear_setup)
+
+
+@torch.library.custom_op(f"{_LIB}::torch_gating_linear", mutates_args=())
+def torch_gating_linear(x: Tensor, weight: Tensor, fp32: bool) -> Tensor:
+    """The reference's gating linear computed by torch itself (F.linear(x, W),
+    or F.linear(x.float(), W.float()) for the DeepSeek router), so the logits
+    and the routing are the reference's bit for bit; its backward is the MFMA
+    kernels' (router_linear_backward: fp32 accumulation, one rounding per
+    gradient)."""
+    return ops.torch_gating_linear(x, weight, fp32)
+
+
+@torch_gating_linear.register_fake
+def _(x, weight, fp32):
+    return x.new_empty(x.shape[0], weight.shape[0],
+                       dtype=torch.float32 if fp32 else x.dtype)
+
+
+def _torch_gating_setup(ctx, inputs, output):
+    x, weight, fp32 = inputs
+    ctx.save_for_backward(x, weight)
+    ctx.out_dtype = torch.float32 if fp32 else x.dtype
+
+
+torch.library.register_autograd(f"{_LIB}::torch_gating_linear", _linear_backward,
+                                setup_context=_torch_gating_setup)
 
 
 # ---------------------------------------------------------- softmax router

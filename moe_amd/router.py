@@ -43,11 +43,14 @@ def gating_linear(x: torch.Tensor, weight: torch.Tensor, fp32: bool, hip: bool =
     """The router's gating linear: bf16 logits (softmax router) or fp32 logits
     (DeepSeek router).  Runs on the MFMA kernel when ``hip`` and both operands
     are bf16 on the GPU (H a multiple of 64, E of 8); otherwise torch's F.linear
-    on the same device."""
+    on the same device (the reference's logits bit for bit), whose backward
+    runs on the MFMA kernels when the operands are bf16 on the GPU."""
     E, H = weight.shape
-    if (hip and x.is_cuda and x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16
-            and H % 64 == 0 and E % 8 == 0):
+    bf = x.is_cuda and x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16
+    if hip and bf and H % 64 == 0 and E % 8 == 0:
         return router_linear(x, weight, torch.float32 if fp32 else torch.bfloat16)
+    if bf:
+        return torch.ops.moe_amd.torch_gating_linear(x, weight, bool(fp32))
     return ops.torch_gating_linear(x, weight, fp32)
 
 

@@ -48,6 +48,10 @@ def test_opcheck_routers():
     torch.library.opcheck(torch.ops.moe_amd.router_linear.default,
                           (x.requires_grad_(True), wr.requires_grad_(True), torch.float32),
                           test_utils=UTILS)
+    for fp32 in (True, False):
+        torch.library.opcheck(torch.ops.moe_amd.torch_gating_linear.default,
+                              (x.detach().requires_grad_(True), wr.detach().requires_grad_(True),
+                               fp32), test_utils=UTILS)
     torch.library.opcheck(torch.ops.moe_amd.softmax_topk.default,
                           (logits.requires_grad_(True), 4, True, None), test_utils=UTILS)
     f32 = logits.detach().float().requires_grad_(True)

@@ -322,3 +322,26 @@ def test_router_fused_nan_rows_and_rejects():
         with pytest.raises(RuntimeError, match="router_softmax_topk"):
             ops.router_linear_softmax_topk(x, wbad, k)
     assert ops.router_linear_softmax_topk(x[:0], wr, K)[2].shape == (0, K)
+
+
+@pytest.mark.parametrize("T,H,E,fp32", [(512, 2048, 1792, True), (1000, 256, 128, False),
+                                        (300, 192, 72, True)])
+def test_torch_gating_linear_op(T, H, E, fp32):
+    """The torch-forward gating op: logits bit-identical to torch's own
+    F.linear (the reference's routing input), gradients from the MFMA
+    backward within one bf16 rounding of the fp64 chain rule (torch's own
+    fp32 fallback where the MFMA shapes do not apply)."""
+    from moe_amd.router import gating_linear
+    print(f"torch gating op T={T} H={H} E={E} fp32={fp32}", flush=True)
+    g = torch.Generator().manual_seed(T + E)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(DEV).requires_grad_(True)
+    wr = (torch.randn(E, H, generator=g) * 0.02).to(torch.bfloat16).to(DEV).requires_grad_(True)
+    lg = gating_linear(x, wr, fp32, hip=False)
+    ref = F.linear(x.detach().float(), wr.detach().float()) if fp32 else F.linear(x.detach(),
+                                                                                  wr.detach())
+    assert lg.dtype == ref.dtype and torch.equal(lg, ref), "logits differ from torch's F.linear"
+    dl = torch.randn(T, E, generator=g).to(lg.dtype).to(DEV)
+    lg.backward(dl)
+    dx_ref = dl.double() @ wr.detach().double()
+    dw_ref = dl.double().t() @ x.detach().double()
+    assert _rel(x.grad, dx_ref) < 1e-2 and _rel(wr.grad, dw_ref) < 1e-2
