@@ -28,6 +28,11 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void softmax_topk_kernel(
     const void* __restrict__ logits, int logits_dtype, const float* __restrict__ offset,
     int64_t T, int E, int K, int renorm, float* __restrict__ probs, float* __restrict__ topk_w,
     int64_t* __restrict__ topk_idx, float* __restrict__ tpe) {
+  // One token per wave (grid_wave), entry j*64 + lane in slot j of a lane.
+  // Registers per lane: the values (two passes: max, then exp/sum/store)
+  // and then only their rank keys; the winners' probs are recomputed from
+  // their keys (key_value returns the value exactly, -0 as +0, which gives
+  // the same exp), bit-identical to the stored row.
   extern __shared__ int hist[];  // [E] when tpe != nullptr
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // token index stays scalar
@@ -36,37 +41,18 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void softmax_topk_kernel(
     __syncthreads();
   }
   const int64_t nwaves = (int64_t)gridDim.x * kWavesPerBlock;
-  // Each wave walks its tokens with the next token's logits already in
-  // flight while the current one is ranked.
-  float raw[NV];
-  auto fetch = [&](int64_t tt) {
+  for (int64_t t = (int64_t)blockIdx.x * kWavesPerBlock + wid; t < T; t += nwaves) {
+    float v[NV];
+    bool nan_here = false;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
       const int e = j * 64 + lane;
-      raw[j] = e < E ? load_logit(logits, logits_dtype, tt * E + e) : 0.f;
+      v[j] = e < E ? load_logit(logits, logits_dtype, t * E + e) + (offset ? offset[e] : 0.0f)
+                   : -INFINITY;
+      nan_here |= v[j] != v[j];
     }
-  };
-  int64_t t = (int64_t)blockIdx.x * kWavesPerBlock + wid;
-  if (t < T) fetch(t);
-  for (; t < T; t += nwaves) {
-    float v[NV];
-    uint64_t taken = 0;
-#pragma unroll
-    for (int j = 0; j < NV; ++j) {
-      int e = j * 64 + lane;
-      if (e < E) {
-        v[j] = raw[j] + (offset ? offset[e] : 0.0f);
-      } else {
-        v[j] = -INFINITY;
-        taken |= 1ull << j;
-      }
-    }
-    if (t + nwaves < T) fetch(t + nwaves);
     // A NaN logit makes every prob of the row NaN, and the reference ranks
     // the probs: the row's entries then all tie and rank by index.
-    bool nan_here = false;
-#pragma unroll
-    for (int j = 0; j < NV; ++j) nan_here |= v[j] != v[j];
     if (__ballot(nan_here)) {
 #pragma unroll
       for (int j = 0; j < NV; ++j)
@@ -76,34 +62,28 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void softmax_topk_kernel(
 #pragma unroll
     for (int j = 0; j < NV; ++j) m = fmaxf(m, v[j]);
     m = wave_max(m);
-    float p[NV];
     float s = 0.f;
 #pragma unroll
-    for (int j = 0; j < NV; ++j) {
-      p[j] = (j * 64 + lane < E) ? expf(v[j] - m) : 0.f;
-      s += p[j];
-    }
+    for (int j = 0; j < NV; ++j) s += (j * 64 + lane < E) ? expf(v[j] - m) : 0.f;
     s = wave_sum(s);
+    uint64_t key[NV];
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-      p[j] = p[j] / s;
-      int e = j * 64 + lane;
-      if (e < E) probs[t * E + e] = p[j];
+      const int e = j * 64 + lane;
+      if (e < E) probs[t * E + e] = expf(v[j] - m) / s;
+      key[j] = e < E ? rank_key(v[j], e) : 0ull;
     }
     // Softmax is monotone, so ranking the (offset) logits ranks the probs;
     // equal logits give bit-equal probs and resolve to the lower expert id.
-    const int ek = wave_topk<NV>(v, taken, lane, K);
-    // Lane k fetches the prob of its selected expert from the owner lane.
-    float wk = 0.f;
-#pragma unroll
-    for (int j = 0; j < NV; ++j) {
-      float pj = __shfl(p[j], ek & 63, 64);
-      if ((ek >> 6) == j) wk = pj;
-    }
+    uint64_t kk;
+    const int ek = wave_topk_keys<NV>(key, lane, K, kk);
+    float wk = lane < K ? expf(key_value(kk) - m) / s : 0.f;
     if (renorm) {
-      // Sum in rank order on every lane (K <= 64 values broadcast one by one).
+      // Sum in rank order on every lane (K <= 64 values read one by one).
       float ssum = 0.f;
-      for (int k = 0; k < K; ++k) ssum += __shfl(wk, k, 64);
+      for (int k = 0; k < K; ++k)
+        ssum += __builtin_bit_cast(float,
+                                   __builtin_amdgcn_readlane(__builtin_bit_cast(int, wk), k));
       wk = wk / ssum;
     }
     if (lane < K) {
@@ -352,35 +332,42 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void sigmoid_topk_kernel(
     __syncthreads();
   }
   const int64_t nwaves = (int64_t)gridDim.x * kWavesPerBlock;
-  // Next token's logits in flight while the current one is ranked.
-  float raw[NV];
-  auto fetch = [&](int64_t tt) {
+  // One token per wave (grid_wave), entry j*64 + lane in slot j of a lane.
+  // The flat selection keeps only the entries' rank keys in registers; the
+  // winners' unbiased scores are recomputed from their logits (the same
+  // function of the same input: bit-identical to the stored scores).
+  for (int64_t t = (int64_t)blockIdx.x * kWavesPerBlock + wid; t < T; t += nwaves) {
+    int ek;
+    if constexpr (!GROUPS) {
+      uint64_t key[NV];
 #pragma unroll
-    for (int j = 0; j < NV; ++j) {
-      const int e = j * 64 + lane;
-      raw[j] = e < E ? logits[tt * E + e] : 0.f;
-    }
-  };
-  int64_t t = (int64_t)blockIdx.x * kWavesPerBlock + wid;
-  if (t < T) fetch(t);
-  for (; t < T; t += nwaves) {
-    float s[NV], b[NV];
-    uint64_t taken = 0;
-#pragma unroll
-    for (int j = 0; j < NV; ++j) {
-      int e = j * 64 + lane;
-      if (e < E) {
-        s[j] = sigmoidf_(raw[j]);
-        scores[t * E + e] = s[j];
-        b[j] = s[j] + (bias ? bias[e] : 0.0f);
-      } else {
-        s[j] = 0.f;
-        b[j] = -INFINITY;
-        taken |= 1ull << j;
+      for (int j = 0; j < NV; ++j) {
+        const int e = j * 64 + lane;
+        if (e < E) {
+          const float sc = sigmoidf_(logits[t * E + e]);
+          scores[t * E + e] = sc;
+          key[j] = rank_key(sc + (bias ? bias[e] : 0.0f), e);
+        } else {
+          key[j] = 0ull;
+        }
       }
-    }
-    if (t + nwaves < T) fetch(t + nwaves);
-    if (GROUPS) {
+      uint64_t kk;
+      ek = wave_topk_keys<NV>(key, lane, K, kk);
+    } else {
+      float b[NV];
+      uint64_t taken = 0;
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        int e = j * 64 + lane;
+        if (e < E) {
+          const float sc = sigmoidf_(logits[t * E + e]);
+          scores[t * E + e] = sc;
+          b[j] = sc + (bias ? bias[e] : 0.0f);
+        } else {
+          b[j] = -INFINITY;
+          taken |= 1ull << j;
+        }
+      }
       // Group-limited selection (router.py:22-70): score each group by the
       // sum of its top (K / group_topk) biased scores, keep group_topk groups.
       const int eg = E / num_groups, per = K / group_topk;
@@ -419,14 +406,9 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void sigmoid_topk_kernel(
         int e = j * 64 + lane;
         if (e < E && !((keep >> (e / eg)) & 1ull)) taken |= 1ull << j;
       }
+      ek = wave_topk<NV>(b, taken, lane, K);
     }
-    const int ek = wave_topk<NV>(b, taken, lane, K);
-    float wk = 0.f;
-#pragma unroll
-    for (int j = 0; j < NV; ++j) {
-      float sj = __shfl(s[j], ek & 63, 64);
-      if ((ek >> 6) == j) wk = sj;
-    }
+    float wk = lane < K ? sigmoidf_(logits[t * E + ek]) : 0.f;
     if (renorm) {
       float ssum = 0.f;
       for (int k = 0; k < K; ++k)
@@ -444,6 +426,76 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void sigmoid_topk_kernel(
       if (tpe && ek >= 0 && ek < E) atomicAdd(&hist[ek], 1);
     }
     __builtin_amdgcn_wave_barrier();
+  }
+  if (tpe) {
+    __syncthreads();
+    for (int e = threadIdx.x; e < E; e += blockDim.x)
+      if (hist[e]) atomicAdd(&tpe[e], (float)hist[e]);
+  }
+}
+
+// DeepSeek router (flat top-k) for large E: one workgroup of four waves per
+// token.  Wave w ranks the entries e = j*256 + w*64 + lane (j < SL): their
+// sigmoid scores are stored, their rank keys (biased score, index) kept in
+// registers, and the wave's K best keys (wave_topk_keys) go to LDS; wave 0
+// then ranks the 4K candidates (one per lane) the same way.  The order is
+// the rank order of every other router kernel, so the selection is the same
+// as the one-wave kernel's; the winners' unbiased scores are recomputed from
+// their logits (bit-identical to the stored scores), renormalised by their
+// sum in rank order (+1e-20), scaled, cast.  K <= 16.
+template <int SL>
+__global__ __launch_bounds__(256) void sigmoid_topk_split_kernel(
+    const float* __restrict__ logits, const float* __restrict__ bias, int64_t T, int E, int K,
+    int renorm, float scaling, float* __restrict__ scores, void* __restrict__ topk_w,
+    int w_dtype, int64_t* __restrict__ topk_idx, float* __restrict__ tpe) {
+  __shared__ uint64_t cand[4 * 16];
+  extern __shared__ int hist[];  // [E] when tpe != nullptr
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (tpe) {
+    for (int e = threadIdx.x; e < E; e += blockDim.x) hist[e] = 0;
+  }
+  for (int64_t t = blockIdx.x; t < T; t += gridDim.x) {
+    const float* lrow = logits + t * E;
+    float* srow = scores + t * E;
+    uint64_t key[SL];
+#pragma unroll
+    for (int j = 0; j < SL; ++j) {
+      const int e = j * 256 + wid * 64 + lane;
+      key[j] = 0ull;
+      if (e < E) {
+        const float sc = sigmoidf_(lrow[e]);
+        srow[e] = sc;
+        key[j] = rank_key(sc + (bias ? bias[e] : 0.0f), e);
+      }
+    }
+    uint64_t mine;
+    wave_topk_keys<SL>(key, lane, K, mine);
+    __syncthreads();  // the previous token's candidates have been read
+    if (lane < K) cand[wid * K + lane] = mine;
+    __syncthreads();
+    if (wid == 0) {
+      uint64_t c[1] = {lane < 4 * K ? cand[lane] : 0ull};
+      uint64_t kk;
+      const int ek = wave_topk_keys<1>(c, lane, K, kk);
+      float wk = lane < K ? sigmoidf_(lrow[ek]) : 0.f;
+      if (renorm) {
+        float ssum = 0.f;
+        for (int k = 0; k < K; ++k)
+          ssum += __builtin_bit_cast(float,
+                                     __builtin_amdgcn_readlane(__builtin_bit_cast(int, wk), k));
+        wk = wk / (ssum + 1e-20f);
+      }
+      if (scaling > 0.f) wk = wk * scaling;
+      if (lane < K) {
+        if (w_dtype == MOE_DTYPE_BF16)
+          ((bf16*)topk_w)[t * K + lane] = f2bf(wk);
+        else
+          ((float*)topk_w)[t * K + lane] = wk;
+        topk_idx[t * K + lane] = ek;
+        if (tpe) atomicAdd(&hist[ek], 1);
+      }
+    }
   }
   if (tpe) {
     __syncthreads();
@@ -716,6 +768,14 @@ int grid_fwd(int64_t T) {
   if (blocks < 1) blocks = 1;
   return (int)blocks;
 }
+// Wave-per-token kernels: one token per wave up to 32768 waves (their
+// rounds are latency-bound chains, so occupancy is what hides them).
+int grid_wave(int64_t T) {
+  int64_t blocks = (T + kWavesPerBlock - 1) / kWavesPerBlock;
+  if (blocks > 8192) blocks = 8192;
+  if (blocks < 1) blocks = 1;
+  return (int)blocks;
+}
 
 #define MOE_DISPATCH_NV(E, KERNEL, ...)                          \
   do {                                                           \
@@ -783,7 +843,7 @@ extern "C" int moe_amd_router_softmax_topk(const void* logits, int logits_dtype,
   else if (G == 16 && V == 8) MOE_SOFTMAX_GROUP(16, 8);
   else if (G == 16) MOE_SOFTMAX_GROUP(16, 16);
   else
-    MOE_DISPATCH_NV(E, softmax_topk_kernel, grid_fwd(T), 64 * kWavesPerBlock, shm,
+    MOE_DISPATCH_NV(E, softmax_topk_kernel, grid_wave(T), 64 * kWavesPerBlock, shm,
                     st >>>(logits, logits_dtype, logit_offset, T, E, K, renormalize, probs,
                            topk_weights, topk_index, tokens_per_expert));
 #undef MOE_SOFTMAX_GROUP
@@ -869,14 +929,30 @@ extern "C" int moe_amd_router_sigmoid_topk(const float* logits, const float* exp
 #undef MOE_SIGMOID_GROUP
     return check_launch("router_sigmoid_topk");
   }
+  if (num_groups <= 0 && E > 256 && K <= 16) {
+    hipStream_t st = (hipStream_t)stream;
+    const int64_t blocks = T < 32768 ? T : 32768;
+#define MOE_SIGMOID_SPLIT(SL_)                                                                \
+  sigmoid_topk_split_kernel<SL_><<<(int)blocks, 256, shm, st>>>(                              \
+      logits, expert_bias, T, E, K, renormalize, scaling_factor, scores, topk_weights,        \
+      weights_dtype, topk_index, tokens_per_expert)
+    const int sl = (E + 255) / 256;
+    if (sl <= 2) MOE_SIGMOID_SPLIT(2);
+    else if (sl <= 4) MOE_SIGMOID_SPLIT(4);
+    else if (sl <= 7) MOE_SIGMOID_SPLIT(7);
+    else if (sl <= 8) MOE_SIGMOID_SPLIT(8);
+    else MOE_SIGMOID_SPLIT(16);
+#undef MOE_SIGMOID_SPLIT
+    return check_launch("router_sigmoid_topk");
+  }
   if (num_groups > 0) {
-    MOE_DISPATCH_NV_G(E, true, sigmoid_topk_kernel, grid_fwd(T), 64 * kWavesPerBlock, shm,
+    MOE_DISPATCH_NV_G(E, true, sigmoid_topk_kernel, grid_wave(T), 64 * kWavesPerBlock, shm,
                       (hipStream_t)stream >>>(logits, expert_bias, T, E, K, renormalize,
                                               scaling_factor, num_groups, group_topk, scores,
                                               topk_weights, weights_dtype, topk_index,
                                               tokens_per_expert));
   } else {
-    MOE_DISPATCH_NV_G(E, false, sigmoid_topk_kernel, grid_fwd(T), 64 * kWavesPerBlock, shm,
+    MOE_DISPATCH_NV_G(E, false, sigmoid_topk_kernel, grid_wave(T), 64 * kWavesPerBlock, shm,
                       (hipStream_t)stream >>>(logits, expert_bias, T, E, K, renormalize,
                                               scaling_factor, num_groups, group_topk, scores,
                                               topk_weights, weights_dtype, topk_index,

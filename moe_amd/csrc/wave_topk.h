@@ -68,21 +68,6 @@ __device__ __forceinline__ void lane_best(const float (&val)[NV], uint64_t taken
   }
 }
 
-// Extracts the K best of val (not in `taken`) in rank order; lane k < K
-// receives the k-th selected expert id (other lanes get 0).
-template <int NV>
-__device__ __forceinline__ int wave_topk(const float (&val)[NV], uint64_t taken, int lane, int K) {
-  int mine = 0;
-  for (int k = 0; k < K; ++k) {
-    float bv;
-    int be;
-    lane_best<NV>(val, taken, lane, bv, be);
-    wave_argmax(bv, be);
-    if (lane == k) mine = be;
-    if ((be & 63) == lane) taken |= 1ull << (be >> 6);
-  }
-  return mine;
-}
 
 // ---------------------------------------------------------------------------
 // Group top-k: G = 8 or 16 consecutive lanes own one row (64/G rows per
@@ -180,4 +165,56 @@ static inline void group_shape(int E, int K, int& G, int& V) {
   const int need = (E + G - 1) / G;
   V = need <= 4 ? 4 : (need <= 8 ? 8 : 16);
 }
+
+// Wave-wide maximum of a 64-bit key: DPP within rows of 16 lanes, then the
+// four row results compared as uniform values.
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t k, int l) {
+  return ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(k >> 32), l) << 32) |
+         (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)k, l);
+}
+
+// Extracts the K best entries in rank order from their rank keys (0 for an
+// entry that takes no part); lane k < K receives the k-th selected expert id
+// and its key (other lanes get 0).  Keys are unique (the index is part of
+// the key), so round k's winner is the largest key below round k-1's
+// winner: each lane takes the minimum of thr-1-key over its entries (keys
+// at or above thr wrap past thr-1 and lose), the wave the maximum of the
+// lanes' results.
+template <int NV>
+__device__ __forceinline__ int wave_topk_keys(const uint64_t (&key)[NV], int lane, int K,
+                                              uint64_t& mine) {
+  uint64_t thr = ~0ull;
+  mine = 0;
+  for (int k = 0; k < K; ++k) {
+    const uint64_t lim = thr - 1;
+    uint64_t d = lim - key[0];
+#pragma unroll
+    for (int j = 1; j < NV; ++j) {
+      const uint64_t dj = lim - key[j];
+      d = dj < d ? dj : d;
+    }
+    uint64_t b = d <= lim ? lim - d : 0ull;
+    b = group_max_key<16>(b);
+    uint64_t w = readlane_u64(b, 0);
+#pragma unroll
+    for (int r = 16; r < 64; r += 16) {
+      const uint64_t o = readlane_u64(b, r);
+      w = o > w ? o : w;
+    }
+    thr = w;
+    mine = lane == k ? w : mine;
+  }
+  return lane < K ? key_index(mine) : 0;
+}
+
+// The same from values (entry j*64 + lane; entries in `taken` take no part).
+template <int NV>
+__device__ __forceinline__ int wave_topk(const float (&val)[NV], uint64_t taken, int lane, int K) {
+  uint64_t key[NV], mine;
+#pragma unroll
+  for (int j = 0; j < NV; ++j)
+    key[j] = ((taken >> j) & 1ull) ? 0ull : rank_key(val[j], j * 64 + lane);
+  return wave_topk_keys<NV>(key, lane, K, mine);
+}
+
 }  // namespace moe

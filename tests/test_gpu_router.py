@@ -85,6 +85,11 @@ def test_torch_topk_tie_order_probe():
     (2000, 512, 128, 8, None, None, None, torch.bfloat16),   # DeepSeek YAMLs' E, flat top-k
     (999, 256, 100, 4, None, None, None, torch.float32),      # lanes partly empty
     (600, 256, 256, 12, None, None, 1.5, torch.bfloat16),     # 16 lanes per token
+    (700, 128, 300, 16, None, None, None, torch.float32),     # 4 waves per token, 2 slots, K=16
+    (333, 128, 520, 8, None, None, 2.0, torch.bfloat16),      # 4 waves per token, ragged slots
+    (100, 64, 4000, 8, None, None, None, torch.float32),      # 4 waves per token, 16 slots
+    (300, 128, 1792, 20, None, None, None, torch.float32),    # K > 16: one wave per token
+    (256, 128, 1792, 8, 8, 4, None, torch.float32),           # grouped at the retrofit E
 ])
 def test_sigmoid_router_parity(T, H, E, K, groups, gtk, sf, wdt):
     print(f"sigmoid router T={T} E={E} K={K} groups={groups}", flush=True)
