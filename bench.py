@@ -146,6 +146,8 @@ def routing_gating_check(cfg, x, wr, inp) -> dict:
     logits come from the MFMA gating kernel instead of torch's F.linear (the
     reference's gating, which the default bench path uses)."""
     from moe_amd import ops
+    if x.dtype != torch.bfloat16:
+        return {"tokens": cfg.T, "hip_gating": "not applicable (fp32 layer: torch gating only)"}
     with torch.no_grad():
         sig = cfg.router == "sigmoid"
         lt = ops.torch_gating_linear(x.detach(), wr.detach(), sig)
@@ -164,6 +166,60 @@ def routing_gating_check(cfg, x, wr, inp) -> dict:
             "hip_gating_logits_differing": logit_diff}
 
 
+def _event_ms(fn, reps: int) -> float:
+    """Mean HIP-event time of fn() on torch's current stream (2 warm-up calls)."""
+    for _ in range(2):
+        fn()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / reps
+
+
+def dense_compare(reps: int = 10) -> dict:
+    """Reference points for the grouped GEMMs: hipBLASLt (torch.matmul, bf16
+    NT) against this library's dense MFMA mode (moe_amd_router_linear, the
+    same template as the grouped GEMMs without the gather) on the dense
+    equivalents of GEMM-1 (N = 2I = 1536, K = H = 2048) and GEMM-2 (N = H =
+    2048, K = I = 768) at the L shape, M = 262144 rows (half of S: the dense
+    mode's 32-bit offsets need M*K*2 < 2^31); the two results compared."""
+    from moe_amd import ops
+    out = {}
+    g = torch.Generator(device="cuda").manual_seed(0)
+    for name, (m, n, k) in {"gemm1_shape": (262144, 1536, 2048),
+                            "gemm2_shape": (262144, 2048, 768)}.items():
+        a = torch.randn(m, k, device="cuda", generator=g).to(torch.bfloat16)
+        b = (torch.randn(n, k, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+        fl = 2.0 * m * n * k
+        t_blas = _event_ms(lambda: a @ b.t(), reps)
+        t_ours = _event_ms(lambda: ops.router_linear(a, b, torch.bfloat16), reps)
+        d = (a @ b.t()).float() - ops.router_linear(a, b, torch.bfloat16).float()
+        out[name] = {"M": m, "N": n, "K": k,
+                     "hipblaslt_ms": round(t_blas, 4),
+                     "hipblaslt_tflops": round(fl / t_blas / 1e9, 1),
+                     "moe_amd_dense_ms": round(t_ours, 4),
+                     "moe_amd_dense_tflops": round(fl / t_ours / 1e9, 1),
+                     "max_abs_diff": float(d.abs().max())}
+        del a, b, d
+    return out
+
+
+def hbm_reference(nbytes: int = 4 << 30, reps: int = 10) -> dict:
+    """Attainable HBM rates with torch's own kernels on this board: a device
+    copy (reads and writes nbytes) and a sum (reads nbytes)."""
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    t_copy = _event_ms(lambda: dst.copy_(src), reps)
+    t_sum = _event_ms(lambda: src.sum(), reps)
+    return {"bytes": nbytes, "copy_ms": round(t_copy, 4),
+            "copy_gbs": round(2 * nbytes / t_copy / 1e6, 1),
+            "sum_ms": round(t_sum, 4), "sum_read_gbs": round(nbytes / t_sum / 1e6, 1)}
+
+
 def copy_calibration(nbytes: int) -> None:
     """A plain copy of known size: reads nbytes, writes nbytes per launch."""
     src = torch.ones(nbytes, dtype=torch.uint8, device="cuda")
@@ -175,26 +231,43 @@ def copy_calibration(nbytes: int) -> None:
     print(json.dumps({"copy_calibration_bytes": nbytes, "launches": 3}), flush=True)
 
 
-# HBM bytes per launch of the six grouped GEMMs at the L shape, measured with
-# rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE (one pass each) and scaled by
-# the same counters on a plain copy of known size (`--copy-calibration`); the
-# commands and per-counter figures are in profiles/gemm_hbm_traffic_L.md.
-RECORDED_TRAFFIC_L = {
-    "gemm_gate_up_swiglu": 9255388063,
-    "gemm_down": 5037341382,
-    "gemm_down_backward_dx_fused": 7960146801,
-    "gemm_down_backward_dw_gathered": 4621847096,
-    "gemm_gate_up_backward_dx": 8214588646,
-    "gemm_gate_up_backward_dw": 6875762976,
-    "router_linear": 302451347,
-    "router_linear_backward_dx": 289924521,
-    "router_linear_backward_dw": 318980091,
+# HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE and --pmc
+# WRITE_SIZE (one pass each) and scaled by the same counters on a plain copy of
+# known size (`--copy-calibration`); the commands and per-counter figures are
+# in profiles/gemm_hbm_traffic_L.md and profiles/retrofit_hbm_traffic.md.
+RECORDED_TRAFFIC = {
+    "L": {
+        "gemm_gate_up_swiglu": 10388933406,
+        "gemm_down": 4715730924,
+        "gemm_down_backward_dx_fused": 7704739493,
+        "gemm_down_backward_dw_gathered": 4451226854,
+        "gemm_gate_up_backward_dx": 8507750279,
+        "gemm_gate_up_backward_dw": 6740456357,
+        "torch_gating_linear": 289695227,
+        "router_linear_backward_dx": 289878683,
+        "router_linear_backward_dw": 318982252,
+    },
+    "Retrofit": {
+        "gemm_gate_up_backward_dw": 12603997810,
+        "gemm_down_backward_dw_gathered": 6582184917,
+        "gemm_gate_up_swiglu": 8420001245,
+        "gemm_gate_up_backward_dx": 7356874577,
+        "gemm_down_backward_dx_fused": 3347306032,
+        "gemm_down": 2463005676,
+        "combine": 605110641,
+        "gather_backward": 604568994,
+        "router_sigmoid_topk": 236835685,
+        "router_sigmoid_topk_backward": 244203891,
+    },
 }
 
 
 def recorded_traffic(cfg_name: str, kernel: str):
-    """Measured HBM bytes per launch of `kernel` (L shape only), else None."""
-    return RECORDED_TRAFFIC_L.get(kernel) if cfg_name.startswith("L") else None
+    """Measured HBM bytes per launch of `kernel` at the L or Retrofit shape, else None."""
+    for key, table in RECORDED_TRAFFIC.items():
+        if cfg_name.startswith(key):
+            return table.get(kernel)
+    return None
 
 
 def probs_for_consumers(cfg, x, wr, inp):
@@ -293,10 +366,16 @@ def main():
                     help="CPU-baseline sample (0: the whole batch, or 128 tokens for banks "
                          "over 2 GB)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--reference-points", action="store_true",
+                    help="time hipBLASLt against the dense MFMA mode on the GEMMs' dense "
+                         "shapes, and torch's copy / sum for attainable HBM rates; no bench")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain device-to-device copy of BYTES (three times): the "
                          "known-size kernel that scales the FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
+    if args.reference_points:
+        print(json.dumps({"dense_gemm": dense_compare(), "hbm": hbm_reference()}), flush=True)
+        return
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
         return

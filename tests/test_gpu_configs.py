@@ -2,7 +2,9 @@
 linear -> router kernel -> permutation -> grouped GEMMs -> combine, and the
 full backward -- on each of the five BASELINE workloads at their full token
 count, against the CPU oracle on the same seeded inputs (configs.make_inputs:
-the fixed CPU draw order, copied to the device), with both gating sources.
+the fixed CPU draw order, copied to the device), with both gating sources
+(torch's F.linear and the MFMA gating kernel; at L and XS-global also the
+router fused into the gating kernel's epilogue).
 
 Per workload and gating source:
   * routing, every token: with the logits the layer used (recomputed by the
@@ -10,8 +12,11 @@ Per workload and gating source:
     bit for bit (softmax router); for the DeepSeek router, selection is exact
     on the kernel's own sigmoid scores and any difference from the oracle's
     end-to-end selection sits on a near-tie of the CPU and GPU sigmoids;
-  * output, d_x (experts' and router's parts together) and the routing-weight
-    gradient of a 256-token sample, recomputed by the oracle from those tokens;
+  * output and d_x (experts' and router's parts together, so the router part
+    carries the routing-weight gradient) of a 256-token sample, recomputed by
+    the oracle from those tokens; d_topk_weights itself, which the one-node
+    layer keeps internal, on M's skewed routing through the expert-layer op
+    (test_layer_routing_weight_grad_sampled);
   * d_gate_up_proj / d_down_proj of the most- and least-loaded experts from
     all their routed rows (each expert's weight gradient depends on its own
     rows only); experts that received no token have exactly zero gradients;
