@@ -35,15 +35,18 @@ static inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; 
 
 // ---- GEMM tile plan (written by the permutation, read by the GEMMs) -----
 // int32 tile_starts[3][E+1]: exclusive prefix of ceil(count_e / BM) for the
-// row-tile heights BM = 64, 128, 256; then, 16-byte aligned, for each BM an
-// int4 table info[ceil(S/BM) + E] = {expert, first row, end row, 0} of
-// every row tile in expert order.
+// row-tile heights BM = 64, 128, 256; int32 row_tile: the index of the height
+// the token-grouped GEMMs run with (the one of least tiles x (BM + 256), the
+// rows and weight columns a 256-column tile streams; the larger on ties);
+// then, 16-byte aligned, for each BM an int4 table info[ceil(S/BM) + E] =
+// {expert, first row, end row, 0} of every row tile in expert order.
 constexpr int kTileSizes[3] = {64, 128, 256};
+static inline size_t plan_row_tile_offset(int E) { return (size_t)3 * (E + 1) * sizeof(int); }
 static inline int64_t plan_max_tiles(int64_t S, int E, int b) {
   return (S + kTileSizes[b] - 1) / kTileSizes[b] + E;
 }
 static inline size_t plan_info_offset(int64_t S, int E, int b) {
-  size_t off = align_up((size_t)3 * (E + 1) * sizeof(int), 16);
+  size_t off = align_up(plan_row_tile_offset(E) + sizeof(int), 16);
   for (int i = 0; i < b; ++i) off += 16 * (size_t)plan_max_tiles(S, E, i);
   return off;
 }

@@ -104,6 +104,8 @@ struct GemmArgs {
   const int* row_src;    // [S]
   const int* offsets;    // [E+1]
   const int* tile_count; // token modes: number of row tiles (tile_starts[E] for BR)
+  const int* row_tile;   // token modes: the plan's chosen row-tile index; a launch whose
+                         // BR is another one returns at once (null: no choice to honour)
   const int4* tile_info; // token modes: {expert, first row, end row, 0} per row tile
   bf16* out;
   bf16* out2;            // gate_up output of G1F (may be null); w * act [S,I] of G2DXF
@@ -222,6 +224,10 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
   constexpr int NTHR = NW * 64;
   constexpr bool TOKEN = MODE <= G1DX || MODE == G2DXF;   // rows = routed rows of one expert
   constexpr bool TRL = MODE == RLT || MODE == RLTK;        // transposed router linear
+  if constexpr (TOKEN) {
+    constexpr int my_tile = BR == 64 ? 0 : (BR == 128 ? 1 : 2);
+    if (p.row_tile && __builtin_amdgcn_readfirstlane(*p.row_tile) != my_tile) return;
+  }
   constexpr bool DENSE = MODE == RL || MODE == RDX || TRL;  // one "expert", dense rows
   constexpr bool COL_KM = !(MODE == G1F || MODE == G2F || MODE == RL || TRL);  // k-major cols
   constexpr bool ROW_KM = !TOKEN && !DENSE;               // row operand k-major (dW)
@@ -1331,25 +1337,35 @@ int pick_br(int64_t S, int E) {
   if (avg >= 128) return 128;
   return 64;
 }
-int tile_index(int br) { return br == 64 ? 0 : (br == 128 ? 1 : 2); }
 
+// Launches a token-grouped GEMM.  With at least 512 routed rows per expert
+// on average every expert that has rows has enough for 256-row tiles, so the
+// host picks them.  Below that the rows per *routed-to* expert decide, which
+// only the device knows: the permutation wrote the height of least streamed
+// bytes into the plan, all three heights are launched, and the two others
+// return at once (one scalar load per workgroup).  Results do not depend on
+// the height: every output element is one k-ordered MFMA chain either way.
 template <int MODE>
 int launch_token(GemmArgs a, int64_t S, int E, int ncols_per_tile_out, int ncols_total,
                  const void* tile_plan, hipStream_t st) {
-  const int br = pick_br(S, E);
-  const int b = tile_index(br);
   const char* pb = (const char*)tile_plan;
-  a.tile_count = (const int*)pb + (size_t)b * (E + 1) + E;
-  a.tile_info = (const int4*)(pb + plan_info_offset(S, E, b));
   a.n_ct = (ncols_total + ncols_per_tile_out - 1) / ncols_per_tile_out;
-  const int64_t max_tiles = plan_max_tiles(S, E, b) * a.n_ct;
-  if (max_tiles > (int64_t)1 << 30) {
-    set_error("grouped_gemm: too many tiles");
-    return MOE_ERR_UNSUPPORTED;
+  const bool device_choice = pick_br(S, E) != 256;
+  a.row_tile = device_choice ? (const int*)(pb + plan_row_tile_offset(E)) : nullptr;
+  for (int b = device_choice ? 0 : 2; b < 3; ++b) {
+    a.tile_count = (const int*)pb + (size_t)b * (E + 1) + E;
+    a.tile_info = (const int4*)(pb + plan_info_offset(S, E, b));
+    const int64_t max_tiles = plan_max_tiles(S, E, b) * a.n_ct;
+    if (max_tiles > (int64_t)1 << 30) {
+      set_error("grouped_gemm: too many tiles");
+      return MOE_ERR_UNSUPPORTED;
+    }
+    const int rc = b == 2 ? launch<MODE, 256>(a, (int)max_tiles, st)
+                 : b == 1 ? launch<MODE, 128>(a, (int)max_tiles, st)
+                          : launch<MODE, 64>(a, (int)max_tiles, st);
+    if (rc != MOE_OK) return rc;
   }
-  if (br == 256) return launch<MODE, 256>(a, (int)max_tiles, st);
-  if (br == 128) return launch<MODE, 128>(a, (int)max_tiles, st);
-  return launch<MODE, 64>(a, (int)max_tiles, st);
+  return MOE_OK;
 }
 int check_common(int64_t S, int E, int H, int I, int dtype, const char* who) {
   MOE_REQUIRE(dtype == MOE_DTYPE_BF16 || dtype == MOE_DTYPE_F32, MOE_ERR_DTYPE,

@@ -125,6 +125,20 @@ __global__ __launch_bounds__(1024) void finalize_kernel(const int* __restrict__ 
       carry[1 + b] += tot;
     }
   }
+  // The row-tile height of the token-grouped GEMMs: the least rows plus
+  // weight columns streamed, tiles x (BM + 256) (the larger height on ties).
+  if (threadIdx.x == 0) {
+    int best = MOE_NUM_TILE_SIZES - 1;
+    int64_t best_cost = (int64_t)carry[best + 1] * (kTileSizes[best] + 256);
+    for (int b = MOE_NUM_TILE_SIZES - 2; b >= 0; --b) {
+      const int64_t c = (int64_t)carry[1 + b] * (kTileSizes[b] + 256);
+      if (c < best_cost) {
+        best = b;
+        best_cost = c;
+      }
+    }
+    tile_starts[MOE_NUM_TILE_SIZES * (E + 1)] = best;
+  }
 }
 
 // Grid (E, 3): fills the row-tile table of expert blockIdx.x for tile height

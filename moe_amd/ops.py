@@ -317,6 +317,13 @@ class RoutingPlan:
         E = self.num_experts
         return self.tile_plan[: 3 * (E + 1) * 4].view(torch.int32).view(3, E + 1)
 
+    @property
+    def row_tile(self) -> torch.Tensor:
+        """The index (into TILE_SIZES) of the row-tile height the token-grouped
+        GEMMs run with, chosen on the device (a one-element int32 tensor)."""
+        E = self.num_experts
+        return self.tile_plan[3 * (E + 1) * 4: 3 * (E + 1) * 4 + 4].view(torch.int32)
+
 
 def permute(topk_index: torch.Tensor, num_experts: int) -> RoutingPlan:
     """Stable counting sort of the routed (token, k) entries by expert."""

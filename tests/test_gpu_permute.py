@@ -78,7 +78,11 @@ def test_tile_plan_tables(T, E, K):
     ref = O.permute(idx, E)
     raw = plan.tile_plan.cpu().numpy()
     S = T * K
-    base = (3 * (E + 1) * 4 + 15) // 16 * 16
+    # the row-tile height: least tiles x (BM + 256), the larger on ties
+    cost = [int(ref.tile_starts[b, E]) * (bm + 256) for b, bm in enumerate(O.TILE_SIZES)]
+    best = min(range(3), key=lambda b: (cost[b], -b))
+    assert int(plan.row_tile.cpu()[0]) == best
+    base = (3 * (E + 1) * 4 + 4 + 15) // 16 * 16
     for b, bm in enumerate(O.TILE_SIZES):
         ntile = int(ref.tile_starts[b, E])
         info = raw[base: base + 16 * ntile].view(np.int32).reshape(ntile, 4)[:, :3]
