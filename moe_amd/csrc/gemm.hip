@@ -247,7 +247,8 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
   static_assert(CPW * NW == 32 && RPW * NW * 8 == BR && TJ >= 1, "DMA blocks per wave");
   // PF: the next tile's first stages are issued before this tile's epilogue,
   // which is wave-local and issues exactly NST stores per wave.
-  constexpr bool PF = MODE == G1F || MODE == G2F || MODE == G1DX || MODE == G1DW || MODE == G2DWG;
+  constexpr bool PF = MODE == G1F || MODE == G2F || MODE == G1DX || MODE == G1DW || MODE == G2DWG ||
+                      MODE == RDX;
   constexpr int NST = (MODE == G1F ? 12 : 8) * TJ;
   static_assert(!PF || CPW + NST <= 63, "vmcnt range");
   static_assert(TOKEN || DENSE || BR == 256, "dW modes use 256-row tiles");
@@ -857,10 +858,11 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
         __builtin_amdgcn_sched_barrier(0);
       }
     } else {
-      // y (G2F), d_xs (G1DX): routed rows x H; d_gate_up_proj[e] (G1DW): 2I x H
+      // y (G2F), d_xs (G1DX): routed rows x H; the gating linear's d_x (RDX):
+      // tokens x H; d_gate_up_proj[e] (G1DW): 2I x H
       int r0, nrows_all;
       const bf16* ob;
-      if constexpr (TOKEN) {
+      if constexpr (TOKEN || MODE == RDX) {
         r0 = c.row0 + ewr * WR;
         nrows_all = c.row_end;
         ob = p.out;
