@@ -394,7 +394,7 @@ def main():
     log(f"[bench] config {cfg.name}: T={cfg.T} H={cfg.H} E={cfg.E} K={cfg.K} I={cfg.I} "
         f"gating={args.gating}")
     inp = make_inputs(cfg, seed=0, device=dev)
-    log("[bench] inputs drawn (CPU, BASELINE order) and resident on the GPU")
+    log("[bench] inputs drawn (CPU, fixed draw order) and resident on the GPU")
     x = inp.x.clone().requires_grad_(True)
     wr = inp.w_router.clone().requires_grad_(True)
     w1 = inp.gate_up_proj.requires_grad_(True)
@@ -483,7 +483,7 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16" if cfg.dtype == torch.bfloat16 else "fp32",
         "data": "synthetic (seeded N(0,1) inputs, N(0,0.02) random-init weights, drawn on the "
-                "CPU in the BASELINE order)",
+                "CPU in a fixed order, per expert)",
         "config": {"workload": f"{cfg.name} MoE layer {'fwd+bwd' if backward else 'fwd'}",
                    "T": cfg.T, "H": cfg.H, "E": cfg.E, "K": cfg.K, "I": cfg.I,
                    "router": cfg.router, "gating": args.gating,

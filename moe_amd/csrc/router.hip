@@ -760,14 +760,6 @@ int grid_for(int64_t T) {
   return (int)blocks;
 }
 
-// Forward routers: about 8 tokens per wave, so that the per-block histogram
-// set-up and flush are amortised and each wave has a next token to prefetch.
-int grid_fwd(int64_t T) {
-  int64_t blocks = (T + kWavesPerBlock * 8 - 1) / (kWavesPerBlock * 8);
-  if (blocks > 4096) blocks = 4096;
-  if (blocks < 1) blocks = 1;
-  return (int)blocks;
-}
 // Wave-per-token kernels: one token per wave up to 32768 waves (their
 // rounds are latency-bound chains, so occupancy is what hides them).
 int grid_wave(int64_t T) {

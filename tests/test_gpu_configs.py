@@ -1,6 +1,6 @@
 """GPU parity of the whole layer as bench.py times it -- ``moe_layer``: gating
 linear -> router kernel -> permutation -> grouped GEMMs -> combine, and the
-full backward -- on each of the five BASELINE workloads at their full token
+full backward -- on each of the five benchmark workloads at their full token
 count, against the CPU oracle on the same seeded inputs (configs.make_inputs:
 the fixed CPU draw order, copied to the device), with both gating sources
 (torch's F.linear and the MFMA gating kernel; at L and XS-global also the
@@ -61,7 +61,7 @@ def _inputs(name):
     if name not in _CACHE:
         _CACHE.clear()  # one workload's inputs resident at a time
         torch.cuda.empty_cache()
-        print(f"[inputs] {name}: drawing on the CPU in the BASELINE order", flush=True)
+        print(f"[inputs] {name}: drawing on the CPU in the fixed draw order", flush=True)
         _CACHE[name] = make_inputs(CONFIGS[name], seed=0, device=DEV)
     return _CACHE[name]
 
