@@ -434,7 +434,10 @@ def main():
     log(f"[bench] {args.steps} steps: {ms:.3f} ms/step (median {step_ms[len(step_ms) // 2]:.3f})")
 
     # Separate pass: the same steps with a HIP-event pair around every
-    # kernel launch, for the per-kernel table and the roofline.
+    # kernel launch, for the per-kernel table and the roofline (with the
+    # recorder installed the layer runs every kernel in order on one stream,
+    # so that each launch is timed alone; the timed steps above overlap the
+    # gather backward with the weight-gradient GEMMs on a second stream).
     events: list = []
     ops.record_kernel_times(events)
     torch.cuda.synchronize()

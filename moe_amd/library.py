@@ -457,6 +457,18 @@ def _(x, w_router, gate_up_proj, down_proj, top_k, renormalize, logit_offset, sa
             x.new_empty(S if save_for_backward else 0, I2)) + _plan_fake(S, E, dev)
 
 
+_SIDE_STREAMS: dict = {}
+
+
+def _side_stream(device: torch.device) -> torch.cuda.Stream:
+    """A second stream per device (default priority), created once."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    s = _SIDE_STREAMS.get(idx)
+    if s is None:
+        s = _SIDE_STREAMS[idx] = torch.cuda.Stream(device=idx)
+    return s
+
+
 @torch.library.custom_op(f"{_LIB}::moe_layer_bwd", mutates_args=())
 def moe_layer_bwd(d_out: Optional[Tensor], d_probs: Optional[Tensor], d_w: Optional[Tensor],
                   x: Tensor, w_router: Tensor, gate_up_proj: Tensor, down_proj: Tensor,
@@ -473,23 +485,43 @@ def moe_layer_bwd(d_out: Optional[Tensor], d_probs: Optional[Tensor], d_w: Optio
         d_out = torch.zeros(x.shape, dtype=x.dtype, device=x.device)
     d_out = d_out.to(x.dtype).contiguous()
     d_gu, act_w, dw = ops.gemm_down_backward_fused(d_out, plan, down_proj, gate_up, w)
+    if d_w is not None:
+        dw = dw + d_w.float()
+    d_logits = ops.router_softmax_topk_backward(probs, idx, dw, d_probs, renormalize,
+                                                torch.bfloat16)
+    d_x = x.new_empty(0)
+    side = None
+    if need_x and ops.kernel_timing_active():
+        # per-launch timing: every kernel in order on the current stream
+        d_xs = ops.gemm_gate_up_backward_dx(d_gu, plan, gate_up_proj)
+        d_x = ops.gather_backward(d_xs, plan,
+                                  addend=ops.router_linear_backward_dx(d_logits, w_router))
+        del d_xs
+    elif need_x:
+        # The gather backward (HBM-bound, no LDS) runs on a second stream
+        # beside the two weight-gradient GEMMs (MFMA-bound, one workgroup per
+        # CU holding its LDS), whose CUs have wave slots and registers left.
+        d_xs = ops.gemm_gate_up_backward_dx(d_gu, plan, gate_up_proj)
+        addend = ops.router_linear_backward_dx(d_logits, w_router)
+        main = torch.cuda.current_stream(x.device)
+        side = _side_stream(x.device)
+        side.wait_stream(main)
+        with torch.cuda.stream(side):
+            d_x = ops.gather_backward(d_xs, plan, addend=addend)
+        for t in (d_xs, addend, counts, offsets, row_src, slot, tile_plan):
+            t.record_stream(side)
+        d_x.record_stream(main)
+        del d_xs, addend
     d_w2 = (ops.gemm_down_backward_dw_gathered(d_out, act_w, plan, down_proj.shape)
             if need_w2 else down_proj.new_empty(0))
     del act_w
     d_w1 = (ops.gemm_gate_up_backward_dw(d_gu, x, plan, gate_up_proj.shape)
             if need_w1 else gate_up_proj.new_empty(0))
-    if d_w is not None:
-        dw = dw + d_w.float()
-    d_logits = ops.router_softmax_topk_backward(probs, idx, dw, d_probs, renormalize,
-                                                torch.bfloat16)
     d_wr = w_router.new_empty(0)
     if need_wr:
         d_wr = ops.router_linear_backward_dw(d_logits, x)
-    d_x = x.new_empty(0)
-    if need_x:
-        d_xs = ops.gemm_gate_up_backward_dx(d_gu, plan, gate_up_proj)
-        d_x = ops.gather_backward(d_xs, plan,
-                                  addend=ops.router_linear_backward_dx(d_logits, w_router))
+    if side is not None:
+        main.wait_stream(side)
     return d_x, d_wr, d_w1, d_w2
 
 

@@ -28,6 +28,11 @@ def record_kernel_times(events: list | None) -> None:
     _events = events
 
 
+def kernel_timing_active() -> bool:
+    """True while record_kernel_times() has a recorder installed."""
+    return _events is not None
+
+
 def _timed(name: str, fn, *args):
     if _events is None:
         return fn(*args)

@@ -96,3 +96,28 @@ def test_compile_fullgraph_matches_eager(layer):
     assert len(eager) == len(comp)
     for a, b in zip(eager, comp):
         assert torch.equal(a, b)
+
+
+def test_layer_backward_overlap_matches_in_order():
+    """The softmax layer's backward with the gather backward on a second
+    stream (beside the weight-gradient GEMMs) gives the same bits as with
+    every kernel in order on one stream (the per-launch timing mode), on
+    three steps in a row."""
+    from moe_amd import ops
+    print("backward overlap vs in order", flush=True)
+    x, wr, w1, w2, _, _, dout = _inputs(T=4096, H=512, E=32, K=4, I=256, seed=7)
+    grads = []
+    for timed in (True, False, False, False):
+        leaves = [t.detach().clone().requires_grad_(True) for t in (x, wr, w1, w2)]
+        if timed:
+            ops.record_kernel_times([])
+        try:
+            out, *_ = moe_layer(*leaves, 4)
+            out.backward(dout)
+        finally:
+            ops.record_kernel_times(None)
+        torch.cuda.synchronize()
+        grads.append([t.grad.clone() for t in leaves])
+    for g in grads[1:]:
+        for a, b in zip(grads[0], g):
+            assert torch.equal(a, b)
