@@ -98,6 +98,39 @@ def _(hidden_states, top_k_index, top_k_weights, gate_up_proj, down_proj, save_f
     return (out, gu, act, y) + _plan_fake(S, E, hidden_states.device)
 
 
+_SIDE_STREAMS: dict = {}
+
+
+def _side_stream(device: torch.device) -> torch.cuda.Stream:
+    """A second stream per device (default priority), created once."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    s = _SIDE_STREAMS.get(idx)
+    if s is None:
+        s = _SIDE_STREAMS[idx] = torch.cuda.Stream(device=idx)
+    return s
+
+
+def _gather_backward_beside(d_xs: Tensor, plan, addend: Optional[Tensor]):
+    """d_x = gather_backward(d_xs, plan, addend) launched on a second stream,
+    after the current stream's work so far, so that it (HBM-bound, no LDS)
+    runs beside the weight-gradient GEMMs the caller launches next (MFMA-
+    bound, one workgroup per CU holding its LDS; their CUs have wave slots and
+    registers left).  Returns (d_x, join): join() makes the current stream
+    wait for it.  With per-launch timing on, it runs in order instead."""
+    if ops.kernel_timing_active():
+        return ops.gather_backward(d_xs, plan, addend=addend), lambda: None
+    main = torch.cuda.current_stream(d_xs.device)
+    side = _side_stream(d_xs.device)
+    side.wait_stream(main)
+    with torch.cuda.stream(side):
+        d_x = ops.gather_backward(d_xs, plan, addend=addend)
+    for t in (d_xs, addend, plan.counts, plan.offsets, plan.row_src, plan.slot, plan.tile_plan):
+        if t is not None:
+            t.record_stream(side)
+    d_x.record_stream(main)
+    return d_x, lambda: main.wait_stream(side)
+
+
 def _experts_bwd_f32(d_out, x, w, w1, w2, gu, act, y, plan, need_x, need_w1, need_w2):
     """fp32: the reference's autograd chain kernel by kernel (combine
     backward -> GEMM-2 dX + dSwiGLU, GEMM-2 dW -> GEMM-1 dW, dX -> gather
@@ -128,15 +161,19 @@ def experts_bwd(d_out: Tensor, hidden_states: Tensor, top_k_weights: Tensor, gat
         return _experts_bwd_f32(d_out, hidden_states, top_k_weights.contiguous(), gate_up_proj,
                                 down_proj, gate_up, act, y, plan, need_x, need_w1, need_w2)
     d_gu, act_w, dw = ops.gemm_down_backward_fused(d_out, plan, down_proj, gate_up, top_k_weights)
+    join = None
+    if need_x:
+        d_x, join = _gather_backward_beside(
+            ops.gemm_gate_up_backward_dx(d_gu, plan, gate_up_proj), plan, None)
+    else:
+        d_x = _empty_like_none(hidden_states)
     d_w2 = (ops.gemm_down_backward_dw_gathered(d_out, act_w, plan, down_proj.shape)
             if need_w2 else _empty_like_none(down_proj))
     del act_w
     d_w1 = (ops.gemm_gate_up_backward_dw(d_gu, hidden_states, plan, gate_up_proj.shape)
             if need_w1 else _empty_like_none(gate_up_proj))
-    if need_x:
-        d_x = ops.gather_backward(ops.gemm_gate_up_backward_dx(d_gu, plan, gate_up_proj), plan)
-    else:
-        d_x = _empty_like_none(hidden_states)
+    if join is not None:
+        join()
     return d_x, dw, d_w1, d_w2
 
 
@@ -457,18 +494,6 @@ def _(x, w_router, gate_up_proj, down_proj, top_k, renormalize, logit_offset, sa
             x.new_empty(S if save_for_backward else 0, I2)) + _plan_fake(S, E, dev)
 
 
-_SIDE_STREAMS: dict = {}
-
-
-def _side_stream(device: torch.device) -> torch.cuda.Stream:
-    """A second stream per device (default priority), created once."""
-    idx = device.index if device.index is not None else torch.cuda.current_device()
-    s = _SIDE_STREAMS.get(idx)
-    if s is None:
-        s = _SIDE_STREAMS[idx] = torch.cuda.Stream(device=idx)
-    return s
-
-
 @torch.library.custom_op(f"{_LIB}::moe_layer_bwd", mutates_args=())
 def moe_layer_bwd(d_out: Optional[Tensor], d_probs: Optional[Tensor], d_w: Optional[Tensor],
                   x: Tensor, w_router: Tensor, gate_up_proj: Tensor, down_proj: Tensor,
@@ -490,28 +515,12 @@ def moe_layer_bwd(d_out: Optional[Tensor], d_probs: Optional[Tensor], d_w: Optio
     d_logits = ops.router_softmax_topk_backward(probs, idx, dw, d_probs, renormalize,
                                                 torch.bfloat16)
     d_x = x.new_empty(0)
-    side = None
-    if need_x and ops.kernel_timing_active():
-        # per-launch timing: every kernel in order on the current stream
+    join = None
+    if need_x:
         d_xs = ops.gemm_gate_up_backward_dx(d_gu, plan, gate_up_proj)
-        d_x = ops.gather_backward(d_xs, plan,
-                                  addend=ops.router_linear_backward_dx(d_logits, w_router))
+        d_x, join = _gather_backward_beside(
+            d_xs, plan, ops.router_linear_backward_dx(d_logits, w_router))
         del d_xs
-    elif need_x:
-        # The gather backward (HBM-bound, no LDS) runs on a second stream
-        # beside the two weight-gradient GEMMs (MFMA-bound, one workgroup per
-        # CU holding its LDS), whose CUs have wave slots and registers left.
-        d_xs = ops.gemm_gate_up_backward_dx(d_gu, plan, gate_up_proj)
-        addend = ops.router_linear_backward_dx(d_logits, w_router)
-        main = torch.cuda.current_stream(x.device)
-        side = _side_stream(x.device)
-        side.wait_stream(main)
-        with torch.cuda.stream(side):
-            d_x = ops.gather_backward(d_xs, plan, addend=addend)
-        for t in (d_xs, addend, counts, offsets, row_src, slot, tile_plan):
-            t.record_stream(side)
-        d_x.record_stream(main)
-        del d_xs, addend
     d_w2 = (ops.gemm_down_backward_dw_gathered(d_out, act_w, plan, down_proj.shape)
             if need_w2 else down_proj.new_empty(0))
     del act_w
@@ -520,8 +529,8 @@ def moe_layer_bwd(d_out: Optional[Tensor], d_probs: Optional[Tensor], d_w: Optio
     d_wr = w_router.new_empty(0)
     if need_wr:
         d_wr = ops.router_linear_backward_dw(d_logits, x)
-    if side is not None:
-        main.wait_stream(side)
+    if join is not None:
+        join()
     return d_x, d_wr, d_w1, d_w2
 
 

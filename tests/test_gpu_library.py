@@ -121,3 +121,25 @@ def test_layer_backward_overlap_matches_in_order():
     for g in grads[1:]:
         for a, b in zip(grads[0], g):
             assert torch.equal(a, b)
+
+
+def test_experts_backward_overlap_matches_in_order():
+    """The same for the expert-layer op (the ExpertsInterface path)."""
+    from moe_amd import ops
+    print("experts backward overlap vs in order", flush=True)
+    x, _, w1, w2, w, idx, dout = _inputs(T=4096, H=512, E=32, K=4, I=256, seed=8)
+    grads = []
+    for timed in (True, False, False):
+        leaves = [t.detach().clone().requires_grad_(True) for t in (x, w, w1, w2)]
+        if timed:
+            ops.record_kernel_times([])
+        try:
+            out = experts_forward(leaves[0], idx, leaves[1], leaves[2], leaves[3])
+            out.backward(dout)
+        finally:
+            ops.record_kernel_times(None)
+        torch.cuda.synchronize()
+        grads.append([t.grad.clone() for t in leaves])
+    for g in grads[1:]:
+        for a, b in zip(grads[0], g):
+            assert torch.equal(a, b)
