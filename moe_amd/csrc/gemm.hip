@@ -497,8 +497,9 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       rstep = BK * 2;
     } else if constexpr (TOKEN || DENSE) {
       const int ld = (MODE == G2F) ? I : ((MODE == G2DX || MODE == RL || TRL) ? H : (MODE == RDX ? p.E : I2));
+      // The tile's own rows only: the extent fits 32 bits whatever S is.
       rptr = (const char*)(p.a0 + (int64_t)d.row0 * ld);
-      rbytes = (uint32_t)((int64_t)(d.row_end - d.row0) * ld * 2);
+      rbytes = (uint32_t)((int64_t)min(d.row_end - d.row0, BR) * ld * 2);
 #pragma unroll
       for (int i = 0; i < RPW; ++i) {
         const int f = kc_feature(wid + NW * i);
@@ -1378,11 +1379,11 @@ int check_common(int64_t S, int E, int H, int I, int dtype, const char* who) {
   MOE_REQUIRE(S >= 0 && E >= 1 && H > 0 && I > 0, MOE_ERR_ARG, "%s: bad sizes", who);
   MOE_REQUIRE(H % 64 == 0 && I % 64 == 0, MOE_ERR_ARG,
               "%s: H=%d and I=%d must be multiples of 64", who, H, I);
-  const int64_t widest = H > 2 * I ? H : 2 * (int64_t)I;
-  // Buffer descriptors address at most one expert's rows (<= S) with
-  // 32-bit byte offsets.
-  MOE_REQUIRE(S * widest * 2 < ((int64_t)1 << 32), MOE_ERR_UNSUPPORTED,
-              "%s: S*max(H,2I) too large for 32-bit buffer offsets", who);
+  // The token-grouped GEMMs address a tile's own rows, the dW GEMMs one
+  // expert's rows (limits at their entry points); row_src is read through a
+  // descriptor of S*4 bytes.
+  MOE_REQUIRE(S < ((int64_t)1 << 29), MOE_ERR_UNSUPPORTED, "%s: S=%lld routed rows, limit 2^29",
+              who, (long long)S);
   MOE_REQUIRE((int64_t)E * H * 2 * I * 2 < ((int64_t)1 << 40), MOE_ERR_ARG, "%s: weights too large",
               who);
   return MOE_OK;
@@ -1883,6 +1884,9 @@ extern "C" int moe_amd_gemm_down_backward_dw(const void* dy, const void* act,
                        (float*)d_down_proj, (hipStream_t)stream);
   int rc = check_common(S, E, H, I, dtype, who);
   if (rc) return rc;
+  // One expert's dy and act rows (at most S) are addressed with 32-bit offsets.
+  MOE_REQUIRE(S * (int64_t)(H > I ? H : I) * 2 < ((int64_t)1 << 32), MOE_ERR_UNSUPPORTED,
+              "%s: S*max(H,I) too large", who);
   MOE_REQUIRE((S == 0 || (dy && act)) && offsets && d_down_proj, MOE_ERR_ARG,
               "%s: null pointer", who);
   if (S > 0) {
@@ -1914,6 +1918,10 @@ extern "C" int moe_amd_gemm_down_backward_dw_gathered(const void* d_out, const v
   if (rc) return rc;
   MOE_REQUIRE(top_k >= 1 && S == T * top_k, MOE_ERR_ARG, "%s: S != T*top_k", who);
   MOE_REQUIRE(T * (int64_t)H * 2 < ((int64_t)1 << 31), MOE_ERR_UNSUPPORTED, "%s: T*H too large",
+              who);
+  // One expert's act_w rows -- at most T, a token's K expert ids being
+  // distinct -- are addressed with 32-bit offsets.
+  MOE_REQUIRE(T * (int64_t)I * 2 < ((int64_t)1 << 32), MOE_ERR_UNSUPPORTED, "%s: T*I too large",
               who);
   MOE_REQUIRE((S == 0 || (d_out && act_w && row_src)) && offsets && d_down_proj, MOE_ERR_ARG,
               "%s: null pointer", who);
@@ -1950,6 +1958,10 @@ extern "C" int moe_amd_gemm_gate_up_backward_dw(const void* d_gate_up, const voi
   if (rc) return rc;
   MOE_REQUIRE(top_k >= 1 && S == T * top_k, MOE_ERR_ARG, "%s: S != T*top_k", who);
   MOE_REQUIRE(T * (int64_t)H * 2 < ((int64_t)1 << 31), MOE_ERR_UNSUPPORTED, "%s: T*H too large",
+              who);
+  // One expert's d_gate_up rows -- at most T, a token's K expert ids being
+  // distinct -- are addressed with 32-bit offsets.
+  MOE_REQUIRE(T * (int64_t)I * 4 < ((int64_t)1 << 32), MOE_ERR_UNSUPPORTED, "%s: T*2I too large",
               who);
   MOE_REQUIRE((S == 0 || (d_gate_up && hidden_states && row_src)) && offsets && d_gate_up_proj,
               MOE_ERR_ARG, "%s: null pointer", who);
