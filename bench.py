@@ -256,16 +256,16 @@ RECORDED_TRAFFIC = {
         "router_linear_backward_dw": 318982252,
     },
     "Retrofit": {
-        "gemm_gate_up_backward_dw": 12603997810,
-        "gemm_down_backward_dw_gathered": 6582184917,
-        "gemm_gate_up_swiglu": 8420001245,
-        "gemm_gate_up_backward_dx": 7356874577,
-        "gemm_down_backward_dx_fused": 3347306032,
-        "gemm_down": 2463005676,
-        "combine": 605110641,
-        "gather_backward": 604568994,
-        "router_sigmoid_topk": 236835685,
-        "router_sigmoid_topk_backward": 244203891,
+        "gemm_gate_up_backward_dw": 12607157703,
+        "gemm_down_backward_dw_gathered": 6583395175,
+        "gemm_gate_up_swiglu": 4202210569,
+        "gemm_gate_up_backward_dx": 4098279500,
+        "gemm_down_backward_dx_fused": 3149835726,
+        "gemm_down": 2185717094,
+        "combine": 605131920,
+        "gather_backward": 604592386,
+        "router_sigmoid_topk": 236797195,
+        "router_sigmoid_topk_backward": 244219508,
     },
 }
 
