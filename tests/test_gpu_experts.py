@@ -54,6 +54,9 @@ CASES = [
     (777, 256, 32, 2, 128, 0.0, 5, torch.float32),      # ragged T, EP sentinels
     (600, 512, 256, 8, 192, 0.0, 0, torch.bfloat16),    # tiny groups, bf16 weights
     (901, 320, 24, 3, 320, 1.0, 7, torch.float32),      # H, I, 2I not multiples of 256
+    (513, 64, 1, 1, 64, 0.0, 0, torch.float32),         # one expert, top-1, smallest H and I
+    (300, 128, 8, 1, 64, 0.0, 0, torch.bfloat16),       # top-1 routing
+    (200, 256, 4, 4, 128, 0.0, 0, torch.float32),       # K = E: every token to every expert
 ]
 
 

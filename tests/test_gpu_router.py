@@ -31,6 +31,9 @@ def _rel(a, b):
     (333, 128, 60, 6, torch.bfloat16),       # ragged sizes
     (1000, 256, 256, 12, torch.bfloat16),    # 16 lanes per token, K > 8
     (777, 128, 200, 8, torch.bfloat16),      # 16 lanes per token, partly empty lanes
+    (100, 64, 1, 1, torch.bfloat16),         # one expert
+    (257, 64, 8, 1, torch.float32),          # top-1
+    (64, 64, 4, 4, torch.bfloat16),          # K = E
 ])
 def test_softmax_router_parity(T, H, E, K, dtype):
     print(f"softmax router T={T} H={H} E={E} K={K} {dtype}", flush=True)
