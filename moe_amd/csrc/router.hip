@@ -718,6 +718,14 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void sigmoid_topk_bwd_kernel(
   __builtin_amdgcn_wave_barrier();
   const int64_t nwaves = (int64_t)gridDim.x * kWavesPerBlock;
   for (int64_t t = (int64_t)blockIdx.x * kWavesPerBlock + wid; t < T; t += nwaves) {
+    // The row's scores are loaded first, so that their latency overlaps
+    // the dependent id -> routed-score loads.
+    float y[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int e = j * 64 + lane;
+      y[j] = e < E ? scores[t * E + e] : 0.f;
+    }
     int ek = lane < K ? (int)idx[t * K + lane] : -1;
     float vk = lane < K ? scores[t * E + ek] : 0.f;
     float gk = 0.f;
@@ -726,12 +734,6 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void sigmoid_topk_bwd_kernel(
                                      : ((const float*)dw)[t * K + lane];
     if (scaling > 0.f) gk *= scaling;
     float dv = renorm ? renorm_backward(vk, gk, K, 1e-20f) : gk;
-    float ds[NV];
-#pragma unroll
-    for (int j = 0; j < NV; ++j) {
-      int e = j * 64 + lane;
-      ds[j] = (e < E && dscores) ? dscores[t * E + e] : 0.f;
-    }
     const bool routed_ok = lane < K && ek >= 0 && ek < E;  // top-k ids are distinct
     if (routed_ok) row[ek] = dv;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -741,8 +743,8 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void sigmoid_topk_bwd_kernel(
     for (int j = 0; j < NV; ++j) {
       int e = j * 64 + lane;
       if (e < E) {
-        float y = scores[t * E + e];
-        dlogits[t * E + e] = (ds[j] + row[e]) * (1.f - y) * y;
+        const float ds = dscores ? dscores[t * E + e] : 0.f;
+        dlogits[t * E + e] = (ds + row[e]) * (1.f - y[j]) * y[j];
       }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
