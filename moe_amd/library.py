@@ -114,9 +114,10 @@ def _gather_backward_beside(d_xs: Tensor, plan, addend: Optional[Tensor]):
     """d_x = gather_backward(d_xs, plan, addend) launched on a second stream,
     after the current stream's work so far, so that it (HBM-bound, no LDS)
     runs beside the weight-gradient GEMMs the caller launches next (MFMA-
-    bound, one workgroup per CU holding its LDS; their CUs have wave slots and
-    registers left).  Returns (d_x, join): join() makes the current stream
-    wait for it.  With per-launch timing on, it runs in order instead."""
+    bound, one workgroup per CU holding all of its LDS and 376-380 of each
+    SIMD's 512 VGPRs per lane; the gather needs no LDS and at most 62 VGPRs, so
+    its waves share those CUs).  Returns (d_x, join): join() makes the current
+    stream wait for it.  With per-launch timing on, it runs in order instead."""
     if ops.kernel_timing_active():
         return ops.gather_backward(d_xs, plan, addend=addend), lambda: None
     main = torch.cuda.current_stream(d_xs.device)
