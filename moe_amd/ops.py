@@ -46,6 +46,12 @@ def _timed(name: str, fn, *args):
 
 
 def _call(name: str, *args) -> None:
+    if torch.cuda.is_current_stream_capturing():
+        # A test that captured the layer's fwd+bwd with torch.cuda.graph
+        # ended the process with a segmentation fault inside the end of the
+        # capture (no GPU fault); until that is understood, refuse capture.
+        raise RuntimeError(f"moe_amd.{name}: HIP graph capture of the moe_amd kernels is not "
+                           "supported; run them eagerly")
     _timed(name, _lib.call, name, *args)
 
 

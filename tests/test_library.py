@@ -84,3 +84,17 @@ def test_experts_and_gradient_trace_into_one_graph():
     targets = {str(n.target) for n in gm.graph.nodes if n.op == "call_function"}
     assert "moe_amd.experts_fwd.default" in targets
     assert "moe_amd.experts_bwd.default" in targets
+
+
+def test_ops_refuse_stream_capture(monkeypatch):
+    """Under stream capture every C-ABI call raises before reaching the
+    library (HIP graph capture is not supported)."""
+    from moe_amd import ops
+
+    def no_call(*args):
+        raise AssertionError("the library was called under capture")
+
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
+    monkeypatch.setattr(_lib, "call", no_call)
+    with pytest.raises(RuntimeError, match="graph capture"):
+        ops._call("moe_amd_permute", 0)
