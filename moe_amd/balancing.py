@@ -27,7 +27,7 @@ from typing import Sequence
 import torch
 
 from . import _lib
-from .ops import _call, _dtype_code, _need_cuda, _stream
+from .ops import _call, _dtype_code, _need_cuda, _stream, on_tensor_device
 
 
 def _contig(t: torch.Tensor) -> torch.Tensor:
@@ -40,6 +40,7 @@ def _as_probs(t: torch.Tensor) -> torch.Tensor:
     return _contig(t)
 
 
+@on_tensor_device
 def topk_stats(probs: torch.Tensor, top_k: int, token_weights: torch.Tensor | None = None):
     """(counts [E] fp64, prob_sums [E] fp64, margin [2] fp64 = sum and min of
     the k-th minus (k+1)-th largest value) of one layer's [T, E] values."""
@@ -90,6 +91,7 @@ class SwitchAuxLoss(torch.autograd.Function):
         return loss.to(layers[0].dtype if layers[0].is_floating_point() else torch.float32)
 
     @staticmethod
+    @on_tensor_device
     def backward(ctx, g):
         coef = _contig(ctx.coef * g.to(torch.float64))
         w = ctx.token_weights
@@ -132,6 +134,7 @@ class SeqAuxLoss(torch.autograd.Function):
     f = E / (K S) * selections.  Gradient through P and the normalisation."""
 
     @staticmethod
+    @on_tensor_device
     def forward(ctx, num_experts, top_k, batch_size, selected, *layers):
         total = None
         ctx.saved = []
@@ -164,6 +167,7 @@ class SeqAuxLoss(torch.autograd.Function):
         return (total / L).to(torch.float32)
 
     @staticmethod
+    @on_tensor_device
     def backward(ctx, g):
         grads = []
         for s, coef, dt in ctx.saved:
@@ -326,9 +330,10 @@ def update_expert_biases(model, update_rate: float, accelerator=None, is_global:
                         dtype=torch.int64, device=dev)
     stats = torch.empty(4, dtype=torch.float64, device=dev)
     L = len(routers)
-    _call("moe_amd_update_expert_biases", ptrs.data_ptr(), ptrs[L:].data_ptr(), L, E,
-          float(update_rate), 1 if is_global else 0, float(alpha) if is_global else 0.0,
-          stats.data_ptr(), _stream(biases[0]))
+    with torch.cuda.device(dev):
+        _call("moe_amd_update_expert_biases", ptrs.data_ptr(), ptrs[L:].data_ptr(), L, E,
+              float(update_rate), 1 if is_global else 0, float(alpha) if is_global else 0.0,
+              stats.data_ptr(), _stream(biases[0]))
     v = stats.cpu().tolist()
     return {"routing/expert_bias_mean": v[0], "routing/expert_bias_std": v[1],
             "routing/expert_bias_min": v[2], "routing/expert_bias_max": v[3]}

@@ -7,6 +7,7 @@ path: non-CUDA tensors or a missing library raise.
 """
 from __future__ import annotations
 
+import functools
 from dataclasses import dataclass
 
 import torch
@@ -43,6 +44,29 @@ def _timed(name: str, fn, *args):
     end.record()
     _events.append((name, start, end))
     return res
+
+
+def _device_of(args, kwargs):
+    for a in (*args, *kwargs.values()):
+        if isinstance(a, RoutingPlan):
+            return a.counts.device
+        if getattr(a, "is_cuda", False):
+            return a.device
+    return None
+
+
+def on_tensor_device(fn):
+    """Runs ``fn`` with the current device set to the device of its first GPU
+    tensor argument: the library launches on the current device, while torch
+    code works on tensors of any device whatever device is current."""
+    @functools.wraps(fn)
+    def run(*args, **kwargs):
+        dev = _device_of(args, kwargs)
+        if dev is None or dev.index is None or dev.index == torch.cuda.current_device():
+            return fn(*args, **kwargs)
+        with torch.cuda.device(dev.index):
+            return fn(*args, **kwargs)
+    return run
 
 
 def _call(name: str, *args) -> None:
@@ -85,6 +109,7 @@ def _contig(t: torch.Tensor) -> torch.Tensor:
 
 # ----------------------------------------------------------------- router
 
+@on_tensor_device
 def torch_gating_linear(x: torch.Tensor, weight: torch.Tensor, fp32: bool) -> torch.Tensor:
     """The reference's own gating linear, as torch computes it on this device:
     ``F.linear(x, W)`` (bf16 logits, src/models/modeling_qwen3_moe.py:268-270)
@@ -98,6 +123,7 @@ def torch_gating_linear(x: torch.Tensor, weight: torch.Tensor, fp32: bool) -> to
     return _timed("torch_gating_linear", run, x, weight)
 
 
+@on_tensor_device
 def router_linear(x: torch.Tensor, weight: torch.Tensor,
                   out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
     """logits [T,E] = x [T,H] . weight [E,H]^T on MFMA (bf16 inputs, fp32
@@ -123,6 +149,7 @@ def router_fused_supported(E: int, top_k: int) -> bool:
     return (64 < E <= 128 and top_k <= 8) or (128 < E <= 256 and top_k <= 16)
 
 
+@on_tensor_device
 def router_linear_softmax_topk(x: torch.Tensor, weight: torch.Tensor, top_k: int,
                                renormalize: bool = True,
                                logit_offset: torch.Tensor | None = None,
@@ -154,6 +181,7 @@ def router_linear_softmax_topk(x: torch.Tensor, weight: torch.Tensor, top_k: int
     return (probs, w, idx, logits) if return_logits else (probs, w, idx)
 
 
+@on_tensor_device
 def router_linear_backward_dx(d_logits: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     """d_x [T,H] = bf16(d_logits [T,E] . weight [E,H]) on MFMA (bf16 inputs)."""
     _need_cuda(d_logits, weight)
@@ -169,6 +197,7 @@ def router_linear_backward_dx(d_logits: torch.Tensor, weight: torch.Tensor) -> t
     return d_x
 
 
+@on_tensor_device
 def router_linear_backward_f32(d_logits: torch.Tensor, x: torch.Tensor, weight: torch.Tensor,
                                need_x: bool = True, need_w: bool = True):
     """(d_x, d_weight) of the fp32 gating linear F.linear(h.float(), W.float())
@@ -200,6 +229,7 @@ def router_linear_backward_f32(d_logits: torch.Tensor, x: torch.Tensor, weight: 
     return d_x, d_w
 
 
+@on_tensor_device
 def router_linear_backward_dw(d_logits: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
     """d_weight [E,H] = bf16(d_logits [T,E]^T . x [T,H]) on MFMA, split over
     token chunks with fp32 partials."""
@@ -219,6 +249,7 @@ def router_linear_backward_dw(d_logits: torch.Tensor, x: torch.Tensor) -> torch.
     return d_w
 
 
+@on_tensor_device
 def router_softmax_topk(logits: torch.Tensor, top_k: int, renormalize: bool = True,
                         logit_offset: torch.Tensor | None = None,
                         tokens_per_expert: torch.Tensor | None = None):
@@ -241,6 +272,7 @@ def router_softmax_topk(logits: torch.Tensor, top_k: int, renormalize: bool = Tr
     return probs, w, idx
 
 
+@on_tensor_device
 def router_softmax_topk_backward(probs, topk_index, d_weights, d_probs, renormalize: bool,
                                  logits_dtype: torch.dtype):
     _need_cuda(probs, topk_index, d_weights, d_probs)
@@ -256,6 +288,7 @@ def router_softmax_topk_backward(probs, topk_index, d_weights, d_probs, renormal
     return d_logits
 
 
+@on_tensor_device
 def router_sigmoid_topk(logits: torch.Tensor, expert_bias: torch.Tensor | None, top_k: int,
                         renormalize: bool = True, scaling_factor: float | None = None,
                         num_groups: int | None = None, group_topk: int | None = None,
@@ -283,6 +316,7 @@ def router_sigmoid_topk(logits: torch.Tensor, expert_bias: torch.Tensor | None, 
     return scores, w, idx
 
 
+@on_tensor_device
 def router_sigmoid_topk_backward(scores, topk_index, d_weights, d_scores, renormalize: bool,
                                  scaling_factor: float | None):
     _need_cuda(scores, topk_index, d_weights, d_scores)
@@ -336,6 +370,7 @@ class RoutingPlan:
         return self.tile_plan[3 * (E + 1) * 4: 3 * (E + 1) * 4 + 4].view(torch.int32)
 
 
+@on_tensor_device
 def permute(topk_index: torch.Tensor, num_experts: int) -> RoutingPlan:
     """Stable counting sort of the routed (token, k) entries by expert."""
     _need_cuda(topk_index)
@@ -365,6 +400,7 @@ def permute(topk_index: torch.Tensor, num_experts: int) -> RoutingPlan:
 
 # --------------------------------------------------------- grouped GEMMs
 
+@on_tensor_device
 def gemm_gate_up_swiglu(x: torch.Tensor, plan: RoutingPlan, gate_up_proj: torch.Tensor,
                         save_gate_up: bool = True):
     """Returns (gate_up [S,2I] or None, act [S,I])."""
@@ -381,6 +417,7 @@ def gemm_gate_up_swiglu(x: torch.Tensor, plan: RoutingPlan, gate_up_proj: torch.
     return gu, act
 
 
+@on_tensor_device
 def gemm_down(act: torch.Tensor, plan: RoutingPlan, down_proj: torch.Tensor) -> torch.Tensor:
     _need_cuda(act, down_proj)
     E, H, I = down_proj.shape
@@ -392,6 +429,7 @@ def gemm_down(act: torch.Tensor, plan: RoutingPlan, down_proj: torch.Tensor) -> 
     return y
 
 
+@on_tensor_device
 def gemm_down_backward_dx_dswiglu(dy, plan: RoutingPlan, down_proj, gate_up):
     _need_cuda(dy, down_proj, gate_up)
     E, H, I = down_proj.shape
@@ -403,6 +441,7 @@ def gemm_down_backward_dx_dswiglu(dy, plan: RoutingPlan, down_proj, gate_up):
     return dgu
 
 
+@on_tensor_device
 def gemm_down_backward_fused(d_out, plan: RoutingPlan, down_proj, gate_up, topk_weights):
     """Backward of the combine and of GEMM-2 + SwiGLU in one GEMM, without
     materialising d_y = w * d_out[token] ([S,H]): per routed row, g = d_out[t]
@@ -431,6 +470,7 @@ def gemm_down_backward_fused(d_out, plan: RoutingPlan, down_proj, gate_up, topk_
     return dgu, act_w, dw
 
 
+@on_tensor_device
 def gemm_down_backward_dw_gathered(d_out, act_w, plan: RoutingPlan, down_proj_shape, out=None,
                                    scheduled: bool = True):
     """d_down_proj[e] = sum over e's rows r of d_out[token(r)]^T act_w[r]
@@ -449,6 +489,7 @@ def gemm_down_backward_dw_gathered(d_out, act_w, plan: RoutingPlan, down_proj_sh
     return dw
 
 
+@on_tensor_device
 def gemm_down_backward_dw(dy, act, plan: RoutingPlan, down_proj_shape, out=None,
                           scheduled: bool = True):
     """d_down_proj [E,H,I].  ``scheduled``: claim tiles from the plan's dW
@@ -463,6 +504,7 @@ def gemm_down_backward_dw(dy, act, plan: RoutingPlan, down_proj_shape, out=None,
     return dw
 
 
+@on_tensor_device
 def gemm_gate_up_backward_dx(dgu, plan: RoutingPlan, gate_up_proj):
     _need_cuda(dgu, gate_up_proj)
     E, I2, H = gate_up_proj.shape
@@ -474,6 +516,7 @@ def gemm_gate_up_backward_dx(dgu, plan: RoutingPlan, gate_up_proj):
     return dxs
 
 
+@on_tensor_device
 def gemm_gate_up_backward_dw(dgu, x, plan: RoutingPlan, gate_up_proj_shape, out=None,
                              scheduled: bool = True):
     """d_gate_up_proj [E,2I,H]; ``scheduled`` as for gemm_down_backward_dw."""
@@ -490,6 +533,7 @@ def gemm_gate_up_backward_dw(dgu, x, plan: RoutingPlan, gate_up_proj_shape, out=
 
 # ---------------------------------------------------------------- combine
 
+@on_tensor_device
 def combine(y: torch.Tensor, plan: RoutingPlan, topk_weights: torch.Tensor) -> torch.Tensor:
     _need_cuda(y, topk_weights)
     topk_weights = _contig(topk_weights)
@@ -502,6 +546,7 @@ def combine(y: torch.Tensor, plan: RoutingPlan, topk_weights: torch.Tensor) -> t
     return out
 
 
+@on_tensor_device
 def combine_backward(d_out, y, plan: RoutingPlan, topk_weights):
     _need_cuda(d_out, y, topk_weights)
     d_out = _contig(d_out)
@@ -516,6 +561,7 @@ def combine_backward(d_out, y, plan: RoutingPlan, topk_weights):
     return dy, dw
 
 
+@on_tensor_device
 def gather_backward(dxs, plan: RoutingPlan, addend: torch.Tensor | None = None) -> torch.Tensor:
     """dx[t] = sum_k dxs[slot[t,k]] (fp32 sum, one rounding); with ``addend``
     [T,H] (same dtype), dx[t] = round(round(sum) + addend[t])."""

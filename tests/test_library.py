@@ -98,3 +98,35 @@ def test_ops_refuse_stream_capture(monkeypatch):
     monkeypatch.setattr(_lib, "call", no_call)
     with pytest.raises(RuntimeError, match="graph capture"):
         ops._call("moe_amd_permute", 0)
+
+
+def test_ops_run_on_their_tensors_device(monkeypatch):
+    """A launching op switches the current device to that of its first GPU
+    tensor (and back) when it differs; with the device already current it
+    switches nothing."""
+    from types import SimpleNamespace
+
+    from moe_amd import ops
+
+    entered = []
+
+    class FakeDevice:
+        def __init__(self, idx):
+            self.idx = idx
+
+        def __enter__(self):
+            entered.append(self.idx)
+
+        def __exit__(self, *exc):
+            return False
+
+    monkeypatch.setattr(torch.cuda, "current_device", lambda: 0)
+    monkeypatch.setattr(torch.cuda, "device", FakeDevice)
+    seen = []
+    op = ops.on_tensor_device(lambda *a, **k: seen.append(list(entered)) or "ran")
+    on1 = SimpleNamespace(is_cuda=True, device=torch.device("cuda", 1))
+    on0 = SimpleNamespace(is_cuda=True, device=torch.device("cuda", 0))
+    assert op(3, on1, x=on0) == "ran" and entered == [1]
+    assert op(on0, on1) == "ran" and entered == [1]          # device 0 already current
+    assert op(torch.zeros(2), k=None) == "ran" and entered == [1]  # no GPU tensor
+    assert seen == [[1], [1], [1]]
