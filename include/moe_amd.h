@@ -154,6 +154,20 @@ int moe_amd_router_sigmoid_topk(const float* logits, const float* expert_bias, i
                                 int weights_dtype, int64_t* topk_index,
                                 float* tokens_per_expert, void* stream);
 
+/* The same router from given scores [T,E] (fp32 values) instead of logits:
+ * the reference's path under bf16 autocast, where F.linear(h.float(),
+ * W.float()) still yields bf16 logits and torch.sigmoid bf16 scores
+ * (src/models/router.py:107-112); the caller passes those scores.  Selection
+ * on scores + expert_bias in fp32 (line 116); the weights follow torch's
+ * bf16 arithmetic of lines 130-138: the sum of the gathered scores rounded to
+ * bf16, + 1e-20 rounded, the quotient and the scaled weight each rounded to
+ * bf16.  Nothing is written back to scores. */
+int moe_amd_router_sigmoid_topk_scores(const float* scores, const float* expert_bias, int64_t T,
+                                       int E, int K, int renormalize, float scaling_factor,
+                                       int num_groups, int group_topk, void* topk_weights,
+                                       int weights_dtype, int64_t* topk_index,
+                                       float* tokens_per_expert, void* stream);
+
 /* Backward of the DeepSeek router's sigmoid -> gather -> renorm -> scale.
  * d_topk_weights is in weights_dtype; d_scores [T,E] fp32 may be NULL.
  * Writes d_logits [T,E] fp32. */

@@ -48,6 +48,8 @@ SIGNATURES: dict[str, tuple] = {
     "moe_amd_router_softmax_topk_backward": (_i, [_p, _p, _p, _p, _i64, _i, _i, _i, _p, _i, _p]),
     "moe_amd_router_sigmoid_topk": (
         _i, [_p, _p, _i64, _i, _i, _i, _f, _i, _i, _p, _p, _i, _p, _p, _p]),
+    "moe_amd_router_sigmoid_topk_scores": (
+        _i, [_p, _p, _i64, _i, _i, _i, _f, _i, _i, _p, _i, _p, _p, _p]),
     "moe_amd_router_sigmoid_topk_backward": (
         _i, [_p, _p, _p, _i, _p, _i64, _i, _i, _i, _f, _p, _p]),
     "moe_amd_permute_workspace_size": (_sz, [_i64, _i]),

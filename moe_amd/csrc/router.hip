@@ -100,6 +100,27 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void softmax_topk_kernel(
   }
 }
 
+// The input of the DeepSeek router kernels: logits (scores = sigmoid,
+// fp32 arithmetic after it: src/models/router.py:107-138), or, with
+// scores_in, the scores themselves -- the reference's torch.sigmoid of bf16
+// logits under bf16 autocast, passed as fp32 values -- after which the
+// weights follow torch's bf16 arithmetic: their sum rounded to bf16 (+1e-20),
+// the quotient and the scaled weight each rounded to bf16.
+__device__ __forceinline__ float dsk_score(float x, int scores_in) {
+  return scores_in ? x : sigmoidf_(x);
+}
+__device__ __forceinline__ float dsk_weight(float v, float ssum, int renorm, float scaling,
+                                            int scores_in) {
+  if (scores_in) {
+    if (renorm) v = round_bf(v / round_bf(round_bf(ssum) + 1e-20f));
+    if (scaling > 0.f) v = round_bf(v * scaling);
+  } else {
+    if (renorm) v = v / (ssum + 1e-20f);
+    if (scaling > 0.f) v = v * scaling;
+  }
+  return v;
+}
+
 // DeepSeek router (flat top-k, no expert groups) with G lanes per token, as
 // softmax_topk_group_kernel: scores = sigmoid(logits) stored, selection by
 // rank keys of the biased scores, the winner's unbiased score taken from its
@@ -110,7 +131,7 @@ template <int G, int V, bool VEC>
 __global__ __launch_bounds__(64 * kWavesPerBlock) void sigmoid_topk_group_kernel(
     const float* __restrict__ logits, const float* __restrict__ bias, int64_t T, int E, int K,
     int renorm, float scaling, float* __restrict__ scores, void* __restrict__ topk_w,
-    int w_dtype, int64_t* __restrict__ topk_idx, float* __restrict__ tpe) {
+    int w_dtype, int64_t* __restrict__ topk_idx, float* __restrict__ tpe, int scores_in) {
   extern __shared__ int hist[];  // [E] when tpe != nullptr
   constexpr int TPW = 64 / G;
   const int lane = threadIdx.x & 63, g = lane & (G - 1), sub = lane / G;
@@ -132,9 +153,9 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void sigmoid_topk_group_kernel
       for (int q = 0; q < V / 4; ++q) {
         const f32x4 a = src[q];
 #pragma unroll
-        for (int h = 0; h < 4; ++h) sc[4 * q + h] = sigmoidf_(a[h]);
+        for (int h = 0; h < 4; ++h) sc[4 * q + h] = dsk_score(a[h], scores_in);
       }
-      if (tok) {
+      if (tok && scores) {
         f32x4* dst = (f32x4*)(scores + t * E + e0);
 #pragma unroll
         for (int q = 0; q < V / 4; ++q)
@@ -144,8 +165,8 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void sigmoid_topk_group_kernel
 #pragma unroll
       for (int j = 0; j < V; ++j) {
         const int e = e0 + j;
-        sc[j] = e < E ? sigmoidf_(logits[tt * E + e]) : 0.f;
-        if (tok && e < E) scores[t * E + e] = sc[j];
+        sc[j] = e < E ? dsk_score(logits[tt * E + e], scores_in) : 0.f;
+        if (tok && e < E && scores) scores[t * E + e] = sc[j];
       }
     }
     uint64_t key[V];
@@ -175,8 +196,7 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void sigmoid_topk_group_kernel
         my_e = key_index(b);
       }
     }
-    if (renorm) my_w = my_w / (ssum + 1e-20f);
-    if (scaling > 0.f) my_w = my_w * scaling;
+    my_w = dsk_weight(my_w, ssum, renorm, scaling, scores_in);
     if (tok && g < K) {
       if (w_dtype == MOE_DTYPE_BF16)
         ((bf16*)topk_w)[t * K + g] = f2bf(my_w);
@@ -323,7 +343,7 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void sigmoid_topk_kernel(
     const float* __restrict__ logits, const float* __restrict__ bias, int64_t T, int E, int K,
     int renorm, float scaling, int num_groups, int group_topk, float* __restrict__ scores,
     void* __restrict__ topk_w, int w_dtype, int64_t* __restrict__ topk_idx,
-    float* __restrict__ tpe) {
+    float* __restrict__ tpe, int scores_in) {
   extern __shared__ int hist[];
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // token index stays scalar
@@ -344,8 +364,8 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void sigmoid_topk_kernel(
       for (int j = 0; j < NV; ++j) {
         const int e = j * 64 + lane;
         if (e < E) {
-          const float sc = sigmoidf_(logits[t * E + e]);
-          scores[t * E + e] = sc;
+          const float sc = dsk_score(logits[t * E + e], scores_in);
+          if (scores) scores[t * E + e] = sc;
           key[j] = rank_key(sc + (bias ? bias[e] : 0.0f), e);
         } else {
           key[j] = 0ull;
@@ -360,8 +380,8 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void sigmoid_topk_kernel(
       for (int j = 0; j < NV; ++j) {
         int e = j * 64 + lane;
         if (e < E) {
-          const float sc = sigmoidf_(logits[t * E + e]);
-          scores[t * E + e] = sc;
+          const float sc = dsk_score(logits[t * E + e], scores_in);
+          if (scores) scores[t * E + e] = sc;
           b[j] = sc + (bias ? bias[e] : 0.0f);
         } else {
           b[j] = -INFINITY;
@@ -408,15 +428,13 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void sigmoid_topk_kernel(
       }
       ek = wave_topk<NV>(b, taken, lane, K);
     }
-    float wk = lane < K ? sigmoidf_(logits[t * E + ek]) : 0.f;
-    if (renorm) {
-      float ssum = 0.f;
+    float wk = lane < K ? dsk_score(logits[t * E + ek], scores_in) : 0.f;
+    float ssum = 0.f;
+    if (renorm)
       for (int k = 0; k < K; ++k)
         ssum += __builtin_bit_cast(float,
                                    __builtin_amdgcn_readlane(__builtin_bit_cast(int, wk), k));
-      wk = wk / (ssum + 1e-20f);
-    }
-    if (scaling > 0.f) wk = wk * scaling;
+    wk = dsk_weight(wk, ssum, renorm, scaling, scores_in);
     if (lane < K) {
       if (w_dtype == MOE_DTYPE_BF16)
         ((bf16*)topk_w)[t * K + lane] = f2bf(wk);
@@ -447,7 +465,7 @@ template <int SL>
 __global__ __launch_bounds__(256) void sigmoid_topk_split_kernel(
     const float* __restrict__ logits, const float* __restrict__ bias, int64_t T, int E, int K,
     int renorm, float scaling, float* __restrict__ scores, void* __restrict__ topk_w,
-    int w_dtype, int64_t* __restrict__ topk_idx, float* __restrict__ tpe) {
+    int w_dtype, int64_t* __restrict__ topk_idx, float* __restrict__ tpe, int scores_in) {
   __shared__ uint64_t cand[4 * 16];
   extern __shared__ int hist[];  // [E] when tpe != nullptr
   const int lane = threadIdx.x & 63;
@@ -464,8 +482,8 @@ __global__ __launch_bounds__(256) void sigmoid_topk_split_kernel(
       const int e = j * 256 + wid * 64 + lane;
       key[j] = 0ull;
       if (e < E) {
-        const float sc = sigmoidf_(lrow[e]);
-        srow[e] = sc;
+        const float sc = dsk_score(lrow[e], scores_in);
+        if (scores) srow[e] = sc;
         key[j] = rank_key(sc + (bias ? bias[e] : 0.0f), e);
       }
     }
@@ -478,15 +496,13 @@ __global__ __launch_bounds__(256) void sigmoid_topk_split_kernel(
       uint64_t c[1] = {lane < 4 * K ? cand[lane] : 0ull};
       uint64_t kk;
       const int ek = wave_topk_keys<1>(c, lane, K, kk);
-      float wk = lane < K ? sigmoidf_(lrow[ek]) : 0.f;
-      if (renorm) {
-        float ssum = 0.f;
+      float wk = lane < K ? dsk_score(lrow[ek], scores_in) : 0.f;
+      float ssum = 0.f;
+      if (renorm)
         for (int k = 0; k < K; ++k)
           ssum += __builtin_bit_cast(float,
                                      __builtin_amdgcn_readlane(__builtin_bit_cast(int, wk), k));
-        wk = wk / (ssum + 1e-20f);
-      }
-      if (scaling > 0.f) wk = wk * scaling;
+      wk = dsk_weight(wk, ssum, renorm, scaling, scores_in);
       if (lane < K) {
         if (w_dtype == MOE_DTYPE_BF16)
           ((bf16*)topk_w)[t * K + lane] = f2bf(wk);
@@ -876,18 +892,19 @@ extern "C" int moe_amd_router_softmax_topk_backward(const float* probs, const in
   return check_launch("router_softmax_topk_backward");
 }
 
-extern "C" int moe_amd_router_sigmoid_topk(const float* logits, const float* expert_bias,
-                                           int64_t T, int E, int K, int renormalize,
-                                           float scaling_factor, int num_groups, int group_topk,
-                                           float* scores, void* topk_weights, int weights_dtype,
-                                           int64_t* topk_index, float* tokens_per_expert,
-                                           void* stream) {
+namespace {
+// Both DeepSeek router entry points: from logits (scores = sigmoid, stored)
+// or, with scores_in, from given scores (logits holds them; scores is null).
+int sigmoid_topk_run(const float* logits, const float* expert_bias, int64_t T, int E, int K,
+                     int renormalize, float scaling_factor, int num_groups, int group_topk,
+                     float* scores, void* topk_weights, int weights_dtype, int64_t* topk_index,
+                     float* tokens_per_expert, void* stream, int scores_in) {
   int rc = check_router_shape(T, E, K);
   if (rc) return rc;
   MOE_REQUIRE(weights_dtype == MOE_DTYPE_F32 || weights_dtype == MOE_DTYPE_BF16, MOE_ERR_DTYPE,
               "router_sigmoid_topk: weights dtype %d", weights_dtype);
-  MOE_REQUIRE(T == 0 || (logits && scores && topk_weights && topk_index), MOE_ERR_ARG,
-              "router_sigmoid_topk: null pointer");
+  MOE_REQUIRE(T == 0 || (logits && (scores || scores_in) && topk_weights && topk_index),
+              MOE_ERR_ARG, "router_sigmoid_topk: null pointer");
   if (num_groups > 0) {
     MOE_REQUIRE(num_groups <= 64 && E % num_groups == 0 && group_topk >= 1 &&
                     group_topk <= num_groups && K % group_topk == 0 &&
@@ -907,7 +924,7 @@ extern "C" int moe_amd_router_sigmoid_topk(const float* logits, const float* exp
 #define MOE_SIGMOID_GROUP(G_, V_, VEC_)                                                       \
   sigmoid_topk_group_kernel<G_, V_, VEC_><<<grid_group(T, G_), 64 * kWavesPerBlock, shm, st>>>( \
       logits, expert_bias, T, E, K, renormalize, scaling_factor, scores, topk_weights,        \
-      weights_dtype, topk_index, tokens_per_expert)
+      weights_dtype, topk_index, tokens_per_expert, scores_in)
 #define MOE_SIGMOID_GROUP_V(G_, V_)            \
   do {                                          \
     if (vec) MOE_SIGMOID_GROUP(G_, V_, true);   \
@@ -929,7 +946,7 @@ extern "C" int moe_amd_router_sigmoid_topk(const float* logits, const float* exp
 #define MOE_SIGMOID_SPLIT(SL_)                                                                \
   sigmoid_topk_split_kernel<SL_><<<(int)blocks, 256, shm, st>>>(                              \
       logits, expert_bias, T, E, K, renormalize, scaling_factor, scores, topk_weights,        \
-      weights_dtype, topk_index, tokens_per_expert)
+      weights_dtype, topk_index, tokens_per_expert, scores_in)
     const int sl = (E + 255) / 256;
     if (sl <= 2) MOE_SIGMOID_SPLIT(2);
     else if (sl <= 4) MOE_SIGMOID_SPLIT(4);
@@ -944,15 +961,38 @@ extern "C" int moe_amd_router_sigmoid_topk(const float* logits, const float* exp
                       (hipStream_t)stream >>>(logits, expert_bias, T, E, K, renormalize,
                                               scaling_factor, num_groups, group_topk, scores,
                                               topk_weights, weights_dtype, topk_index,
-                                              tokens_per_expert));
+                                              tokens_per_expert, scores_in));
   } else {
     MOE_DISPATCH_NV_G(E, false, sigmoid_topk_kernel, grid_wave(T), 64 * kWavesPerBlock, shm,
                       (hipStream_t)stream >>>(logits, expert_bias, T, E, K, renormalize,
                                               scaling_factor, num_groups, group_topk, scores,
                                               topk_weights, weights_dtype, topk_index,
-                                              tokens_per_expert));
+                                              tokens_per_expert, scores_in));
   }
   return check_launch("router_sigmoid_topk");
+}
+}  // namespace
+
+extern "C" int moe_amd_router_sigmoid_topk(const float* logits, const float* expert_bias,
+                                           int64_t T, int E, int K, int renormalize,
+                                           float scaling_factor, int num_groups, int group_topk,
+                                           float* scores, void* topk_weights, int weights_dtype,
+                                           int64_t* topk_index, float* tokens_per_expert,
+                                           void* stream) {
+  return sigmoid_topk_run(logits, expert_bias, T, E, K, renormalize, scaling_factor, num_groups,
+                          group_topk, scores, topk_weights, weights_dtype, topk_index,
+                          tokens_per_expert, stream, 0);
+}
+
+extern "C" int moe_amd_router_sigmoid_topk_scores(const float* scores, const float* expert_bias,
+                                                  int64_t T, int E, int K, int renormalize,
+                                                  float scaling_factor, int num_groups,
+                                                  int group_topk, void* topk_weights,
+                                                  int weights_dtype, int64_t* topk_index,
+                                                  float* tokens_per_expert, void* stream) {
+  return sigmoid_topk_run(scores, expert_bias, T, E, K, renormalize, scaling_factor, num_groups,
+                          group_topk, nullptr, topk_weights, weights_dtype, topk_index,
+                          tokens_per_expert, stream, 1);
 }
 
 extern "C" int moe_amd_router_sigmoid_topk_backward(const float* scores,

@@ -375,9 +375,18 @@ def sigmoid_topk(logits: Tensor, expert_bias: Optional[Tensor], top_k: int, reno
     The counts come back as an output (the op is functional); the router adds
     them to its local_tokens_per_expert buffer."""
     counts = torch.zeros(logits.shape[1], device=logits.device, dtype=torch.float32)
-    scores, w, idx = ops.router_sigmoid_topk(
-        logits, expert_bias, top_k, renormalize, scaling_factor or None,
-        num_groups or None, group_topk or None, weights_dtype, counts if count else None)
+    if logits.dtype == torch.float32:
+        scores, w, idx = ops.router_sigmoid_topk(
+            logits, expert_bias, top_k, renormalize, scaling_factor or None,
+            num_groups or None, group_topk or None, weights_dtype, counts if count else None)
+    else:
+        # bf16 logits: the reference under bf16 autocast, whose fp32 gating
+        # linear still yields bf16 logits; its torch.sigmoid then gives bf16
+        # scores (router.py:112), computed here by the same torch call.
+        scores = torch.sigmoid(logits)
+        w, idx = ops.router_sigmoid_topk_scores(
+            scores, expert_bias, top_k, renormalize, scaling_factor or None,
+            num_groups or None, group_topk or None, weights_dtype, counts if count else None)
     return scores, w, idx, counts
 
 
@@ -386,7 +395,7 @@ def _(logits, expert_bias, top_k, renormalize, scaling_factor, num_groups, group
       weights_dtype, count):
     T, E = logits.shape
     dev = logits.device
-    return (torch.empty(T, E, device=dev, dtype=torch.float32),
+    return (torch.empty(T, E, device=dev, dtype=logits.dtype),
             torch.empty(T, top_k, device=dev, dtype=weights_dtype),
             torch.empty(T, top_k, device=dev, dtype=torch.int64),
             torch.empty(E, device=dev, dtype=torch.float32))
@@ -396,9 +405,9 @@ def _(logits, expert_bias, top_k, renormalize, scaling_factor, num_groups, group
 def sigmoid_topk_backward(scores: Tensor, topk_index: Tensor, d_weights: Tensor,
                           d_scores: Optional[Tensor], renormalize: bool,
                           scaling_factor: float) -> Tensor:
-    """d_logits [T,E] fp32 (autograd of router.py:112-140)."""
+    """d_logits [T,E] in the scores' dtype (autograd of router.py:112-140)."""
     return ops.router_sigmoid_topk_backward(scores, topk_index, d_weights, d_scores, renormalize,
-                                            scaling_factor or None)
+                                            scaling_factor or None).to(scores.dtype)
 
 
 @sigmoid_topk_backward.register_fake

@@ -317,9 +317,39 @@ def router_sigmoid_topk(logits: torch.Tensor, expert_bias: torch.Tensor | None, 
 
 
 @on_tensor_device
+def router_sigmoid_topk_scores(scores: torch.Tensor, expert_bias: torch.Tensor | None,
+                               top_k: int, renormalize: bool = True,
+                               scaling_factor: float | None = None,
+                               num_groups: int | None = None, group_topk: int | None = None,
+                               weights_dtype: torch.dtype = torch.bfloat16,
+                               tokens_per_expert: torch.Tensor | None = None):
+    """DeepSeek-V3 routing from given scores (the reference's torch.sigmoid
+    of bf16 logits under bf16 autocast, src/models/router.py:107-140): the
+    same selection, weights in torch's bf16 arithmetic.  Returns (weights
+    [T,K] in weights_dtype, index int64 [T,K])."""
+    _need_cuda(scores, expert_bias, tokens_per_expert)
+    s32 = _contig(scores.to(torch.float32))
+    T, E = s32.shape
+    dev = s32.device
+    w = torch.empty(T, top_k, device=dev, dtype=weights_dtype)
+    idx = torch.empty(T, top_k, device=dev, dtype=torch.int64)
+    if expert_bias is not None:
+        expert_bias = _contig(expert_bias.to(torch.float32))
+    grouped = num_groups is not None and group_topk is not None
+    _call("moe_amd_router_sigmoid_topk_scores", s32.data_ptr(), _ptr(expert_bias), T, E, top_k,
+          int(renormalize), float(scaling_factor or 0.0), int(num_groups) if grouped else 0,
+          int(group_topk) if grouped else 0, w.data_ptr(), _dtype_code(weights_dtype),
+          idx.data_ptr(), _ptr(tokens_per_expert), _stream(s32))
+    return w, idx
+
+
+@on_tensor_device
 def router_sigmoid_topk_backward(scores, topk_index, d_weights, d_scores, renormalize: bool,
                                  scaling_factor: float | None):
+    """d_logits [T,E] fp32 through the gather / renorm / scaling and the
+    sigmoid (d scores * (1 - y) * y, y the scores, read as fp32)."""
     _need_cuda(scores, topk_index, d_weights, d_scores)
+    scores = _contig(scores.to(torch.float32))
     T, E = scores.shape
     K = topk_index.shape[1]
     d_weights = _contig(d_weights)

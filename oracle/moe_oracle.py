@@ -99,10 +99,29 @@ def sigmoid_router(logits: torch.Tensor, expert_bias: torch.Tensor | None, top_k
                    renormalize: bool = True, scaling_factor: float | None = None,
                    num_groups: int | None = None, group_topk: int | None = None,
                    weights_dtype: torch.dtype = torch.float32):
-    """DeepSeekRouter after its fp32 F.linear (router.py:111-140).
-    Returns (scores [T,E] fp32, weights [T,K] weights_dtype, index int64)."""
-    scores = torch.sigmoid(logits.float())
-    biased = scores + (expert_bias.float() if expert_bias is not None else 0.0)
+    """DeepSeekRouter after its gating linear (router.py:111-140).  fp32
+    logits: the fp32 path.  bf16 logits: the same lines as torch runs them
+    under bf16 autocast (whose F.linear(h.float(), W.float()) returns bf16):
+    torch.sigmoid keeps bf16 (:112).  Returns (scores [T,E] in the logits'
+    floating dtype (fp32 unless bf16), weights [T,K] weights_dtype, index
+    int64)."""
+    lp = logits.dtype == torch.bfloat16
+    scores = torch.sigmoid(logits if lp else logits.float())
+    w, idx = sigmoid_router_from_scores(scores, expert_bias, top_k, renormalize, scaling_factor,
+                                        num_groups, group_topk, weights_dtype)
+    return scores, w, idx
+
+
+def sigmoid_router_from_scores(scores: torch.Tensor, expert_bias: torch.Tensor | None,
+                               top_k: int, renormalize: bool = True,
+                               scaling_factor: float | None = None,
+                               num_groups: int | None = None, group_topk: int | None = None,
+                               weights_dtype: torch.dtype = torch.float32):
+    """router.py:114-140 on given scores, in the scores' dtype as torch
+    evaluates those lines: the biased scores fp32 (scores + fp32 bias, :116),
+    the gathered weights, their sum (+1e-20), quotient and scaling in the
+    scores' dtype (bf16 for bf16 scores).  Returns (weights, index)."""
+    biased = scores.float() + (expert_bias.float() if expert_bias is not None else 0.0)
     if num_groups is not None and group_topk is not None:
         _, idx = group_limited_topk(biased, top_k, num_groups, group_topk)
     else:
@@ -112,7 +131,7 @@ def sigmoid_router(logits: torch.Tensor, expert_bias: torch.Tensor | None, top_k
         w = w / (w.sum(dim=-1, keepdim=True) + 1e-20)
     if scaling_factor:
         w = w * scaling_factor
-    return scores, w.to(weights_dtype), idx
+    return w.to(weights_dtype), idx
 
 
 def softmax_router_backward(probs, idx, d_w, d_probs, renormalize: bool, logits_dtype):

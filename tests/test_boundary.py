@@ -293,3 +293,66 @@ def test_global_bank_dispatches_through_experts_interface():
     e2 = (bank.down_proj.grad.double().cpu() - acc2).abs().max() / acc2.abs().max()
     print(f"global bank dW over two calls: {e1:.2e} {e2:.2e}", flush=True)
     assert e1 < 2e-2 and e2 < 2e-2
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("router", ["softmax", "deepseek"])
+def test_tiny_hf_model_under_bf16_autocast(router):
+    """The reference's training precision: fp32 parameters (the model is
+    built from its config and never cast, train.py:193-235) and the forward
+    under bf16 autocast (Accelerator(mixed_precision="bf16"), train.py:395-400).
+    The gating linear then yields bf16 logits; the routing must be the
+    reference's on them and the experts run in the weights' fp32, as
+    transformers' grouped_mm does (it casts the input to the weight dtype).
+    The second block's output is checked against the oracle at the fp32
+    bound, and every parameter gradient is fp32 and finite."""
+    import torch.nn.functional as F
+
+    from oracle import moe_oracle as O
+    from moe_amd import hf
+    from moe_amd.router import MI355XDeepSeekRouter
+    print(f"tiny HF model under bf16 autocast, {router} router", flush=True)
+    m = _tiny_model().to("cuda")
+    cfg = m.config
+    if router == "deepseek":
+        g = torch.Generator().manual_seed(3)
+        for layer in m.model.layers:
+            new = MI355XDeepSeekRouter(cfg).to("cuda")
+            new.weight = layer.mlp.gate.weight
+            new.expert_bias.copy_((torch.rand(cfg.num_experts, generator=g) - 0.5).to("cuda"))
+            layer.mlp.gate = new
+    hf.install(m)
+    blk = m.model.layers[1].mlp
+    captured = []
+    blk.register_forward_hook(lambda mod, inp, out: captured.append((inp[0].detach(),
+                                                                     out.detach())))
+    ids = torch.randint(0, 256, (2, 32), device="cuda")
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        out = m(ids, labels=ids)
+    out.loss.backward()
+    assert torch.isfinite(out.loss)
+    for p in (blk.experts.gate_up_proj, blk.experts.down_proj, blk.gate.weight):
+        assert p.grad is not None and p.grad.dtype == torch.float32
+        assert torch.isfinite(p.grad).all()
+    h, y = captured[0]
+    flat = h.reshape(-1, cfg.hidden_size)
+    K = cfg.num_experts_per_tok
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        if router == "softmax":
+            logits = F.linear(flat, blk.gate.weight)
+        else:
+            logits = F.linear(flat.float(), blk.gate.weight.float())
+    assert logits.dtype == torch.bfloat16
+    if router == "softmax":
+        _, w, idx = O.softmax_router(logits.cpu(), K)
+    else:
+        w, idx = O.sigmoid_router_from_scores(torch.sigmoid(logits).cpu(),
+                                              blk.gate.expert_bias.cpu(), K, True,
+                                              weights_dtype=flat.dtype)
+    # the experts compute in the weights' dtype (fp32), their input cast to it
+    ref, _ = O.experts_forward(flat.float().cpu(), idx, w, blk.experts.gate_up_proj.detach().cpu(),
+                               blk.experts.down_proj.detach().cpu())
+    assert y.dtype == flat.dtype
+    err = (y.reshape(-1, cfg.hidden_size).double().cpu() - ref.double()).abs().max() \
+        / ref.abs().max()
+    assert err < 1e-5, float(err)

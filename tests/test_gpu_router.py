@@ -180,6 +180,53 @@ def test_sigmoid_router_backward_parity(E, K, wdt):
     assert torch.allclose(gl.cpu(), ref, rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("T,E,K,groups,gtk,sf,renorm,wdt", [
+    (2048, 128, 8, None, None, None, True, torch.bfloat16),   # group kernel, 16-byte rows
+    (777, 100, 6, None, None, 2.5, True, torch.float32),      # group kernel, element rows
+    (512, 1792, 8, None, None, None, True, torch.bfloat16),   # four waves per token
+    (300, 256, 8, 8, 4, None, True, torch.float32),           # group-limited, wave per token
+    (400, 2304, 20, None, None, None, False, torch.bfloat16),  # K > 16: wave per token
+])
+def test_sigmoid_router_bf16_scores_parity(T, E, K, groups, gtk, sf, renorm, wdt):
+    """The DeepSeek router from bf16 scores (the reference under bf16
+    autocast): index and weights bit-identical to the oracle's evaluation of
+    router.py:114-140 on the same scores, counts exact."""
+    print(f"sigmoid router from bf16 scores T={T} E={E} K={K} groups={groups}", flush=True)
+    g = torch.Generator().manual_seed(T + E + 7)
+    logits = (torch.randn(T, E, generator=g) * 2).to(torch.bfloat16).to(DEV)
+    bias = ((torch.rand(E, generator=g) * 2 - 1) * 0.5).to(DEV)
+    scores = torch.sigmoid(logits)
+    tpe = torch.zeros(E, device=DEV)
+    w, idx = ops.router_sigmoid_topk_scores(scores, bias, K, renorm, sf, groups, gtk, wdt, tpe)
+    torch.cuda.synchronize()
+    w_ref, i_ref = O.sigmoid_router_from_scores(scores.cpu(), bias.cpu(), K, renorm, sf, groups,
+                                                gtk, wdt)
+    assert torch.equal(idx.cpu(), i_ref)
+    assert torch.equal(w.cpu(), w_ref)
+    assert torch.equal(tpe.cpu(), torch.bincount(i_ref.reshape(-1), minlength=E).float())
+
+
+def test_sigmoid_layer_op_takes_bf16_logits():
+    """moe_amd::sigmoid_topk on bf16 logits: bf16 scores as torch.sigmoid
+    gives them, the from-scores selection, and a backward through the
+    sigmoid in the logits' dtype."""
+    g = torch.Generator().manual_seed(5)
+    T, E, K = 1024, 128, 8
+    logits = torch.randn(T, E, generator=g).to(torch.bfloat16).to(DEV).requires_grad_(True)
+    bias = (torch.rand(E, generator=g) - 0.5).to(DEV)
+    scores, w, idx = sigmoid_topk(logits, bias, K, True, None, None, None, torch.bfloat16, None)
+    assert scores.dtype == torch.bfloat16 and torch.equal(scores, torch.sigmoid(logits))
+    w_ref, i_ref = O.sigmoid_router_from_scores(scores.detach().cpu(), bias.cpu(), K, True,
+                                                weights_dtype=torch.bfloat16)
+    assert torch.equal(idx.cpu(), i_ref) and torch.equal(w.cpu(), w_ref)
+    dw = torch.randn(T, K, generator=g).to(DEV)
+    (gl,) = torch.autograd.grad((w.float() * dw).sum(), logits)
+    ref = O.sigmoid_router_backward(scores.detach().float().cpu(), idx.cpu(),
+                                    dw.to(torch.bfloat16).float().cpu(), None, True, None)
+    assert gl.dtype == torch.bfloat16
+    assert _rel(gl.float(), ref) < 1e-2  # bf16 rounding of the gradient
+
+
 @pytest.mark.parametrize("T,H,E", [
     (65536, 2048, 128),   # L router GEMM
     (4096, 2048, 1792),   # retrofit expert count (token sample)

@@ -122,6 +122,31 @@ def test_sigmoid_router_reference_properties():
     assert torch.equal(wb, w.to(torch.bfloat16))
 
 
+def test_sigmoid_router_bf16_scores_known_answers():
+    """The router's lines evaluated on bf16 scores (the reference under bf16
+    autocast): hand-derived values."""
+    # renormalisation in bf16: 0.5 / 0.75 and 0.25 / 0.75 each rounded to
+    # 8 significant bits (1.0101011b x 2^-1 and x 2^-2); they sum to 1.0019531
+    s = torch.tensor([[0.5, 0.25, 0.125, 0.0625]], dtype=torch.bfloat16)
+    w, idx = O.sigmoid_router_from_scores(s, None, 2, True, None, weights_dtype=torch.float32)
+    assert idx.tolist() == [[0, 1]]
+    assert w.tolist() == [[0.66796875, 0.333984375]]
+    w32, _ = O.sigmoid_router_from_scores(s.float(), None, 2, True, None)
+    assert torch.allclose(w32, torch.tensor([[2 / 3, 1 / 3]]))
+    assert w32.tolist() != w.tolist()
+    # scores are rounded before the bias is added: 0.75 + 2^-12 and 0.75 are
+    # one bf16 value, so the 2^-14 bias of expert 1 decides; in fp32 expert 0
+    # stays ahead by 2^-12 - 2^-14
+    s32 = torch.tensor([[0.75 + 2.0 ** -12, 0.75]])
+    bias = torch.tensor([0.0, 2.0 ** -14])
+    _, i32 = O.sigmoid_router_from_scores(s32, bias, 1, True)
+    _, i16 = O.sigmoid_router_from_scores(s32.to(torch.bfloat16), bias, 1, True)
+    assert i32.tolist() == [[0]] and i16.tolist() == [[1]]
+    # bf16 logits keep bf16 scores (torch.sigmoid leaves the dtype)
+    sc, _, _ = O.sigmoid_router(torch.zeros(2, 8, dtype=torch.bfloat16), None, 2)
+    assert sc.dtype == torch.bfloat16 and torch.equal(sc.float(), torch.full((2, 8), 0.5))
+
+
 def test_group_limited_topk_constraints():
     g = torch.Generator().manual_seed(42)
     scores = torch.randn(128, 32, generator=g).abs()
