@@ -366,15 +366,32 @@ def _sched_tables(plan, S, E):
     return v[:32].reshape(2, 16), v[32:41], v[48:48 + E]
 
 
+def _check_sched(plan, S, E):
+    """The dW schedule tables are well-formed: reset queue counters, every
+    expert once, balanced XCD ranges and the serpentine bound on the XCDs'
+    rows.  Returns the per-XCD rows."""
+    queue, xstart, xorder = _sched_tables(plan, S, E)
+    assert not queue.any()                       # reset after each launch
+    assert sorted(xorder.tolist()) == list(range(E))
+    n = np.diff(xstart)
+    assert xstart[0] == 0 and xstart[8] == E and n.max() - n.min() <= 1
+    counts = plan.counts.cpu().numpy()
+    load = [counts[xorder[xstart[i]:xstart[i + 1]]].sum() for i in range(8)]
+    assert max(load) <= sum(load) / 8 + counts.max() + 1   # serpentine dealing bound
+    return load
+
+
 @pytest.mark.parametrize("T,H,E,K,I,skew", [
     (4096, 1024, 128, 8, 256, 3.0),   # Zipf-like skew, empty experts
     (1500, 512, 13, 4, 256, 2.0),     # E not a multiple of the 8 XCDs
     (700, 256, 5, 2, 256, 0.0),       # fewer experts than XCDs
 ])
 def test_dw_schedule_matches_static_walk(T, H, E, K, I, skew):
-    """The dW GEMMs' claimed-tile schedule covers every tile exactly once:
-    bit-identical to the static walk, on two launches in a row (the last
-    workgroup resets the queue counters), with balanced, well-formed tables."""
+    """The dW GEMMs' claimed-tile schedule covers every tile exactly once,
+    the zero tiles of the experts without rows included: bit-identical to the
+    static walk, on two launches in a row (the last workgroup resets the
+    queue counters) into NaN-filled outputs, with balanced, well-formed
+    tables."""
     print(f"dW schedule T={T} H={H} E={E} K={K} I={I} skew={skew}", flush=True)
     x, idx, w, w1, w2, _ = _inputs(T, H, E, K, I, T + E + 3, skew)
     S = T * K
@@ -384,21 +401,20 @@ def test_dw_schedule_matches_static_walk(T, H, E, K, I, skew):
     act = torch.randn(S, I, generator=g).to(torch.bfloat16).to(DEV)
     dgu = torch.randn(S, 2 * I, generator=g).to(torch.bfloat16).to(DEV)
     xd = x.to(DEV)
+    dout = torch.randn(T, H, generator=g).to(torch.bfloat16).to(DEV)
     ref2 = ops.gemm_down_backward_dw(dy, act, plan, (E, H, I), scheduled=False)
     ref1 = ops.gemm_gate_up_backward_dw(dgu, xd, plan, (E, 2 * I, H), scheduled=False)
+    ref3 = ops.gemm_down_backward_dw_gathered(dout, act, plan, (E, H, I), scheduled=False)
+    nan = float("nan")
     for _ in range(2):
-        d2 = ops.gemm_down_backward_dw(dy, act, plan, (E, H, I))
-        d1 = ops.gemm_gate_up_backward_dw(dgu, xd, plan, (E, 2 * I, H))
+        d2 = ops.gemm_down_backward_dw(dy, act, plan, (E, H, I), out=torch.full_like(ref2, nan))
+        d1 = ops.gemm_gate_up_backward_dw(dgu, xd, plan, (E, 2 * I, H),
+                                          out=torch.full_like(ref1, nan))
+        d3 = ops.gemm_down_backward_dw_gathered(dout, act, plan, (E, H, I),
+                                                out=torch.full_like(ref3, nan))
         torch.cuda.synchronize()
-        assert torch.equal(d2, ref2) and torch.equal(d1, ref1)
-    queue, xstart, xorder = _sched_tables(plan, S, E)
-    assert not queue.any()                       # reset after each launch
-    assert sorted(xorder.tolist()) == list(range(E))
-    n = np.diff(xstart)
-    assert xstart[0] == 0 and xstart[8] == E and n.max() - n.min() <= 1
-    counts = plan.counts.cpu().numpy()
-    load = [counts[xorder[xstart[i]:xstart[i + 1]]].sum() for i in range(8)]
-    assert max(load) <= sum(load) / 8 + counts.max() + 1   # serpentine dealing bound
+        assert torch.equal(d2, ref2) and torch.equal(d1, ref1) and torch.equal(d3, ref3)
+    _check_sched(plan, S, E)
 
 
 @pytest.mark.parametrize("path", ["experts", "softmax_layer", "sigmoid_layer"])
