@@ -194,12 +194,16 @@ def dense_compare(reps: int = 10) -> dict:
     same template as the grouped GEMMs without the gather) on the dense
     equivalents of GEMM-1 (N = 2I = 1536, K = H = 2048) and GEMM-2 (N = H =
     2048, K = I = 768) at the L shape, M = 262144 rows (half of S: the dense
-    mode's 32-bit offsets need M*K*2 < 2^31); the two results compared."""
+    mode's 32-bit offsets need M*K*2 < 2^31), and on two square shapes
+    (8192^3, 16384^3: long K, few tiles' prologues and epilogues per FLOP,
+    the board's MFMA ceiling with either kernel); the two results compared."""
     from moe_amd import ops
     out = {}
     g = torch.Generator(device="cuda").manual_seed(0)
     for name, (m, n, k) in {"gemm1_shape": (262144, 1536, 2048),
-                            "gemm2_shape": (262144, 2048, 768)}.items():
+                            "gemm2_shape": (262144, 2048, 768),
+                            "square_8192": (8192, 8192, 8192),
+                            "square_16384": (16384, 16384, 16384)}.items():
         a = torch.randn(m, k, device="cuda", generator=g).to(torch.bfloat16)
         b = (torch.randn(n, k, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
         fl = 2.0 * m * n * k
