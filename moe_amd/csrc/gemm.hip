@@ -526,12 +526,20 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
   };
 
   // G1DW, G2DWG: raw row_src entries of stage s, one 64-lane load per wave
-  // (lane L: k row L of the stage); a column block's two k rows are read
-  // out of it with v_readlane when its DMA offsets are formed.  Reads past S
-  // return zero; rows past the expert's range are masked there.
+  // (lane L: k row L of the stage).  Reads past S return zero.
   auto fetch_tok = [&](int s, int (&tk)[NTOK > 0 ? NTOK : 1]) {
     if constexpr (GCOL)
       tk[0] = __builtin_amdgcn_raw_buffer_load_b32(isrc, (uint32_t)(kb_cur + s * BK + lane) * 4, 0, 0);
+  };
+  // ... turned in place, once the load has landed, into the byte offset of
+  // each k row's token row (token * H * 2), or kOOB for rows past the
+  // expert's range; a column block's two k rows are then read out of it
+  // with v_readlane when its DMA offsets are formed.
+  auto tok_offsets = [&](int s, int (&tk)[NTOK > 0 ? NTOK : 1]) {
+    if constexpr (GCOL) {
+      const bool ok = s * BK + lane < ke_cur - kb_cur;
+      tk[0] = (int)(ok ? (uint32_t)div_topk(tk[0], p.tok_mul, p.tok_shift) * (uint32_t)(H * 2) : kOOB);
+    }
   };
 
   auto slot_ptr = [&](int h) { return (char*)smem + (h % NSLOT) * SLOT; };
@@ -539,15 +547,14 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
   // DMA of the column half of stage s (ring position 2s).
   auto col_off = [&](int s, int i, const int (&tk)[NTOK > 0 ? NTOK : 1]) -> uint32_t {
     if constexpr (GCOL) {
+      // tk: stage s's row offsets (tok_offsets).  A kOOB row stays at or
+      // above kOOB plus the column offset (< 2^31), beyond the operand's
+      // extent (T * H * 2 < 2^31), so it reads zeros.
+      (void)s;
       const int blk = wid + NW * i;  // wave-uniform: k rows 2*blk and 2*blk+1
-      const int kr = s * BK + km_krow(blk);
-      const int ta = __builtin_amdgcn_readlane(tk[0], 2 * blk);
-      const int tb = __builtin_amdgcn_readlane(tk[0], 2 * blk + 1);
-      const int src = (lane >> 5) ? tb : ta;
-      // Branch-free select (rows past the expert's range read zeros).
-      const uint32_t v = (uint32_t)div_topk(src, p.tok_mul, p.tok_shift) * (uint32_t)(H * 2) + coff[i];
-      const uint32_t m = 0u - (uint32_t)(kr < ke_cur - kb_cur);
-      return (v & m) | (kOOB & ~m);
+      const uint32_t ta = (uint32_t)__builtin_amdgcn_readlane(tk[0], 2 * blk);
+      const uint32_t tb = (uint32_t)__builtin_amdgcn_readlane(tk[0], 2 * blk + 1);
+      return ((lane >> 5) ? tb : ta) + coff[i];
     } else {
       return coff[i];
     }
@@ -596,28 +603,32 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
   // operand once (opaque to the optimizer, which would otherwise fold the
   // sub-step constants into the scalar slot base and re-add per read); the
   // sub-step and sub-tile parts then ride in the instructions' offsets.
-  const lds_char_t* const lds0 = (const lds_char_t*)smem;
+  // The addresses are absolute LDS byte addresses: the base of the dynamic
+  // LDS array (a link-time constant the compiler would otherwise add to
+  // every read) is folded into the scalar slot base once per step.
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(const lds_char_t*)smem;
+  auto lds_at = [](uint32_t a) { return (const lds_char_t*)(uintptr_t)a; };
   uint32_t a_adr[4], b_adr[4];
   auto slot_bases = [&](uint32_t sC, uint32_t sR) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      a_adr[q] = opaque_add(sC, a_off[q]);
-      b_adr[q] = opaque_add(sR, b_off[q]);
+      a_adr[q] = opaque_add(lds0 + sC, a_off[q]);
+      b_adr[q] = opaque_add(lds0 + sR, b_off[q]);
     }
   };
   auto read_a = [&](int ks, int i) -> bf16x8 {
     if constexpr (!COL_KM) {
-      return *(const __attribute__((address_space(3))) bf16x8*)(lds0 + a_adr[ks] + i * 4096);
+      return *(const __attribute__((address_space(3))) bf16x8*)lds_at(a_adr[ks] + i * 4096);
     } else {
-      const lds_char_t* q = lds0 + a_adr[i] + ks * (16 * BC * 2);
+      const lds_char_t* q = lds_at(a_adr[i] + ks * (16 * BC * 2));
       return tr_frag(q, q + 4 * BC * 2);
     }
   };
   auto read_b = [&](int ks, int j) -> bf16x8 {
     if constexpr (!ROW_KM) {
-      return *(const __attribute__((address_space(3))) bf16x8*)(lds0 + b_adr[ks] + j * 4096);
+      return *(const __attribute__((address_space(3))) bf16x8*)lds_at(b_adr[ks] + j * 4096);
     } else {
-      const lds_char_t* q = lds0 + b_adr[j] + ks * (16 * BR * 2);
+      const lds_char_t* q = lds_at(b_adr[j] + ks * (16 * BR * 2));
       return tr_frag(q, q + 4 * BR * 2);
     }
   };
@@ -641,11 +652,13 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       // scheduler from interleaving the groups.
       fetch_tok(0, tk_a);
       fetch_tok(1, tk_b);
+      tok_offsets(0, tk_a);
       issue_col(0, tk_a);
       __builtin_amdgcn_sched_barrier(0);
       fetch_tok(2, tk_a);
       issue_row(0);
       __builtin_amdgcn_sched_barrier(0);
+      tok_offsets(1, tk_b);
       issue_col(1, tk_b);
       if constexpr (MODE == G2DXF) {
         // The row's routing weight, in flight under the main loop (raw bits:
@@ -698,6 +711,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
         WAIT_VMCNT_LGKM0(CPW);
       }
       __builtin_amdgcn_s_barrier();  // B(0)
+      tok_offsets(2, tk_a);  // its load is older than stage 0's DMA
       slot_bases(0, (uint32_t)SLOT);
 #pragma unroll
       for (int i = 0; i < TI; ++i) fa[0][i] = read_a(0, i);
@@ -724,12 +738,13 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
             for (int j = 0; j < TJ; ++j)
               acc[i][j] = mma(fa[ks & 1][i], fb[ks & 1][j], acc[i][j]);
             group_order();
-            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_sched_barrier(0x4);
           }
         }
         if constexpr (NTOK > 0) {
 #pragma unroll
           for (int i = 0; i < NTOK; ++i) tk_a[i] = tn[i];  // row_src entries of stage kt+3
+          tok_offsets(kt + 3, tk_a);  // their load opened this stage's window
         }
         constexpr int LB = GQ & 1;  // fragment buffer of the last sub-step
         static_assert(LB == 1, "sub-step 0 of the next stage reads into buffer 0");
@@ -752,7 +767,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
           for (int j = 0; j < TJ; ++j)
             acc[i][j] = mma(fa[1][i], fb[1][j], acc[i][j]);
           group_order();
-          __builtin_amdgcn_sched_barrier(0);
+          __builtin_amdgcn_sched_barrier(0x4);
         }
       }
   };
