@@ -674,8 +674,14 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
   // tile's epilogue stores were issued after this tile's prologue (PF modes).
   auto mainloop = [&](const Tile& cur, bool after_epi) {
     (void)after_epi;
-      // Op o of window W(w); `tk` holds the row_src entries of stage w+2.
-      auto win_op = [&](int w, int o, const int (&tk)[NTOK > 0 ? NTOK : 1]) {
+      // Byte offsets of ring positions 2kt + c, c = 0..4, at stage kt.  The
+      // positions advance by two per stage, so the five offsets rotate by
+      // two at the end of each stage (register moves, not a modulo).
+      uint32_t rq[5] = {0, SLOT, 2 * SLOT, 3 * SLOT, 4 * SLOT};
+      // Op o of window W(w) (its row half lands at ring offset srow, its
+      // column half at scol); `tk` holds the row_src entries of stage w+2.
+      auto win_op = [&](int w, int o, const int (&tk)[NTOK > 0 ? NTOK : 1], uint32_t srow,
+                        uint32_t scol) {
         if (o < NTOK) {
           if constexpr (GCOL)
             tn[0] = __builtin_amdgcn_raw_buffer_load_b32(
@@ -683,11 +689,11 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
         } else if (o < NTOK + RPW) {
           const int i = o - NTOK;
           const auto rs = stage_rsrc(rptr, rbytes, kst(w + 1) * rstep, w + 1);
-          dma16(rs, roff[i], slot_ptr(2 * w + 3) + (wid + NW * i) * 1024);
+          dma16(rs, roff[i], (char*)smem + srow + (wid + NW * i) * 1024);
         } else {
           const int i = o - NTOK - RPW;
           const auto rs = stage_rsrc(cptr, cbytes, kst(w + 2) * cstep, w + 2);
-          dma16(rs, col_off(w + 2, i, tk), slot_ptr(2 * w + 4) + (wid + NW * i) * 1024);
+          dma16(rs, col_off(w + 2, i, tk), (char*)smem + scol + (wid + NW * i) * 1024);
         }
       };
       // Issue order inside an MFMA group: two MFMAs, the group's memory
@@ -720,7 +726,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       // the part of W(0) that belongs to the (absent) last sub-step of stage -1
 #pragma unroll
       for (int o = 0; o < TI * NOPS / NGRP; ++o) {
-        win_op(0, o, tk_a);
+        win_op(0, o, tk_a, rq[3], rq[4]);  // ring positions 3 and 4
         __builtin_amdgcn_sched_barrier(0);
       }
       for (int kt = 0; kt < cur.nk; ++kt) {
@@ -731,7 +737,8 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
           for (int i = 0; i < TI; ++i) {
             const int q = TI + ks * TI + i;
 #pragma unroll
-            for (int o = q * NOPS / NGRP; o < (q + 1) * NOPS / NGRP; ++o) win_op(kt, o, tk_a);
+            for (int o = q * NOPS / NGRP; o < (q + 1) * NOPS / NGRP; ++o)
+              win_op(kt, o, tk_a, rq[3], rq[4]);  // positions 2kt+3, 2kt+4
             fa[(ks + 1) & 1][i] = read_a(ks + 1, i);
             if (i < TJ) fb[(ks + 1) & 1][i] = read_b(ks + 1, i);
 #pragma unroll
@@ -754,13 +761,14 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
         // the window after it are junk, kept to make every iteration alike.)
         WAIT_VMCNT_LGKM0(CPW);
         __builtin_amdgcn_s_barrier();  // B(kt+1)
-        slot_bases((uint32_t)((2 * kt + 2) % NSLOT) * SLOT, (uint32_t)((2 * kt + 3) % NSLOT) * SLOT);
+        slot_bases(rq[2], rq[3]);  // stage kt+1: positions 2kt+2, 2kt+3
         // Last sub-step of stage kt, groups 0..TI-1 of W(kt+1), and the
         // fragments of sub-step 0 of stage kt+1.
 #pragma unroll
         for (int i = 0; i < TI; ++i) {
 #pragma unroll
-          for (int o = i * NOPS / NGRP; o < (i + 1) * NOPS / NGRP; ++o) win_op(kt + 1, o, tk_a);
+          for (int o = i * NOPS / NGRP; o < (i + 1) * NOPS / NGRP; ++o)
+            win_op(kt + 1, o, tk_a, rq[0], rq[1]);  // positions 2kt+5, 2kt+6
           fa[0][i] = read_a(0, i);
           if (i < TJ) fb[0][i] = read_b(0, i);
 #pragma unroll
@@ -769,6 +777,12 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
           group_order();
           __builtin_amdgcn_sched_barrier(0x4);
         }
+        const uint32_t r0 = rq[0], r1 = rq[1];
+        rq[0] = rq[2];
+        rq[1] = rq[3];
+        rq[2] = rq[4];
+        rq[3] = r0;
+        rq[4] = r1;
       }
   };
 
