@@ -537,8 +537,10 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
   // with v_readlane when its DMA offsets are formed.
   auto tok_offsets = [&](int s, int (&tk)[NTOK > 0 ? NTOK : 1]) {
     if constexpr (GCOL) {
-      const bool ok = s * BK + lane < ke_cur - kb_cur;
-      tk[0] = (int)(ok ? (uint32_t)div_topk(tk[0], p.tok_mul, p.tok_shift) * (uint32_t)(H * 2) : kOOB);
+      // Branch-free select (a branch would mask lanes and wait on the load).
+      const uint32_t v = (uint32_t)div_topk(tk[0], p.tok_mul, p.tok_shift) * (uint32_t)(H * 2);
+      const uint32_t m = 0u - (uint32_t)(s * BK + lane < ke_cur - kb_cur);
+      tk[0] = (int)((v & m) | (kOOB & ~m));
     }
   };
 
@@ -678,22 +680,26 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       // positions advance by two per stage, so the five offsets rotate by
       // two at the end of each stage (register moves, not a modulo).
       uint32_t rq[5] = {0, SLOT, 2 * SLOT, 3 * SLOT, 4 * SLOT};
-      // Op o of window W(w) (its row half lands at ring offset srow, its
-      // column half at scol); `tk` holds the row_src entries of stage w+2.
+      // Op o of window W(w): its row half (stage w+1, descriptor rsr) lands at
+      // ring offset srow, its column half (stage w+2, descriptor rsc) at
+      // scol; `tk` holds the row_src entries of stage w+2.  A window begins
+      // in the last sub-step of the stage before, so its row descriptor is
+      // formed once there and carried into the next iteration.
+      static_assert(TI * NOPS / NGRP <= NTOK + RPW, "a window's first TI groups hold no column op");
+      auto row_rsrc = [&](int s) { return stage_rsrc(rptr, rbytes, kst(s) * rstep, s); };
+      auto col_rsrc = [&](int s) { return stage_rsrc(cptr, cbytes, kst(s) * cstep, s); };
       auto win_op = [&](int w, int o, const int (&tk)[NTOK > 0 ? NTOK : 1], uint32_t srow,
-                        uint32_t scol) {
+                        uint32_t scol, __amdgpu_buffer_rsrc_t rsr, __amdgpu_buffer_rsrc_t rsc) {
         if (o < NTOK) {
           if constexpr (GCOL)
             tn[0] = __builtin_amdgcn_raw_buffer_load_b32(
                 isrc, (uint32_t)(kb_cur + (w + 3) * BK + lane) * 4, 0, 0);
         } else if (o < NTOK + RPW) {
           const int i = o - NTOK;
-          const auto rs = stage_rsrc(rptr, rbytes, kst(w + 1) * rstep, w + 1);
-          dma16(rs, roff[i], (char*)smem + srow + (wid + NW * i) * 1024);
+          dma16(rsr, roff[i], (char*)smem + srow + (wid + NW * i) * 1024);
         } else {
           const int i = o - NTOK - RPW;
-          const auto rs = stage_rsrc(cptr, cbytes, kst(w + 2) * cstep, w + 2);
-          dma16(rs, col_off(w + 2, i, tk), (char*)smem + scol + (wid + NW * i) * 1024);
+          dma16(rsc, col_off(w + 2, i, tk), (char*)smem + scol + (wid + NW * i) * 1024);
         }
       };
       // Issue order inside an MFMA group: two MFMAs, the group's memory
@@ -724,12 +730,14 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
 #pragma unroll
       for (int j = 0; j < TJ; ++j) fb[0][j] = read_b(0, j);
       // the part of W(0) that belongs to the (absent) last sub-step of stage -1
+      __amdgpu_buffer_rsrc_t rs_row = row_rsrc(1);  // W(0)'s row half: stage 1
 #pragma unroll
       for (int o = 0; o < TI * NOPS / NGRP; ++o) {
-        win_op(0, o, tk_a, rq[3], rq[4]);  // ring positions 3 and 4
+        win_op(0, o, tk_a, rq[3], rq[4], rs_row, rs_row);  // ring positions 3 and 4 (no column op)
         __builtin_amdgcn_sched_barrier(0);
       }
       for (int kt = 0; kt < cur.nk; ++kt) {
+        const __amdgpu_buffer_rsrc_t rs_col = col_rsrc(kt + 2);
         // Sub-steps 0..2 of stage kt; groups TI..NGRP-1 of W(kt).
 #pragma unroll
         for (int ks = 0; ks < GQ; ++ks) {
@@ -738,7 +746,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
             const int q = TI + ks * TI + i;
 #pragma unroll
             for (int o = q * NOPS / NGRP; o < (q + 1) * NOPS / NGRP; ++o)
-              win_op(kt, o, tk_a, rq[3], rq[4]);  // positions 2kt+3, 2kt+4
+              win_op(kt, o, tk_a, rq[3], rq[4], rs_row, rs_col);  // positions 2kt+3, 2kt+4
             fa[(ks + 1) & 1][i] = read_a(ks + 1, i);
             if (i < TJ) fb[(ks + 1) & 1][i] = read_b(ks + 1, i);
 #pragma unroll
@@ -764,11 +772,12 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
         slot_bases(rq[2], rq[3]);  // stage kt+1: positions 2kt+2, 2kt+3
         // Last sub-step of stage kt, groups 0..TI-1 of W(kt+1), and the
         // fragments of sub-step 0 of stage kt+1.
+        rs_row = row_rsrc(kt + 2);
 #pragma unroll
         for (int i = 0; i < TI; ++i) {
 #pragma unroll
           for (int o = i * NOPS / NGRP; o < (i + 1) * NOPS / NGRP; ++o)
-            win_op(kt + 1, o, tk_a, rq[0], rq[1]);  // positions 2kt+5, 2kt+6
+            win_op(kt + 1, o, tk_a, rq[0], rq[1], rs_row, rs_row);  // positions 2kt+5, 2kt+6
           fa[0][i] = read_a(0, i);
           if (i < TJ) fb[0][i] = read_b(0, i);
 #pragma unroll
