@@ -249,15 +249,15 @@ def copy_calibration(nbytes: int) -> None:
 # in profiles/gemm_hbm_traffic_L.md and profiles/retrofit_hbm_traffic.md.
 RECORDED_TRAFFIC = {
     "L": {
-        "gemm_gate_up_swiglu": 10505492071,
-        "gemm_down": 4683664632,
-        "gemm_down_backward_dx_fused": 7984564107,
-        "gemm_down_backward_dw_gathered": 4598725512,
-        "gemm_gate_up_backward_dx": 8475859950,
-        "gemm_gate_up_backward_dw": 6926095265,
-        "torch_gating_linear": 289694146,
-        "router_linear_backward_dx": 290605050,
-        "router_linear_backward_dw": 318966844,
+        "gemm_gate_up_swiglu": 10491262144,
+        "gemm_down": 4685523502,
+        "gemm_down_backward_dx_fused": 8045133370,
+        "gemm_down_backward_dw_gathered": 4585666743,
+        "gemm_gate_up_backward_dx": 8300821229,
+        "gemm_gate_up_backward_dw": 6902455435,
+        "torch_gating_linear": 289694415,
+        "router_linear_backward_dx": 290591268,
+        "router_linear_backward_dw": 318966255,
     },
     "Retrofit": {
         "gemm_gate_up_backward_dw": 12607157703,
