@@ -713,6 +713,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       };
       constexpr int GQ = BK / 16 - 1;  // groups before the last sub-step: NGRP - TI
+      constexpr int NLR = TI + TJ;     // fragment reads of a sub-step
       bf16x8 fa[2][TI], fb[2][TJ];
       if constexpr (PF) {
         // the previous tile's NST epilogue stores were issued after this
@@ -747,8 +748,18 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
 #pragma unroll
             for (int o = q * NOPS / NGRP; o < (q + 1) * NOPS / NGRP; ++o)
               win_op(kt, o, tk_a, rq[3], rq[4], rs_row, rs_col);  // positions 2kt+3, 2kt+4
-            fa[(ks + 1) & 1][i] = read_a(ks + 1, i);
-            if (i < TJ) fb[(ks + 1) & 1][i] = read_b(ks + 1, i);
+            if (ks + 1 < GQ) {
+              fa[(ks + 1) & 1][i] = read_a(ks + 1, i);
+              if (i < TJ) fb[(ks + 1) & 1][i] = read_b(ks + 1, i);
+            } else {
+              // The last sub-step's fragments, read in the groups before the
+              // last one: the barrier's lgkmcnt(0) then finds them landed.
+#pragma unroll
+              for (int r = i * NLR / (TI - 1); r < (i + 1) * NLR / (TI - 1) && r < NLR; ++r) {
+                if (r < TI) fa[1][r] = read_a(GQ, r);
+                else fb[1][r - TI] = read_b(GQ, r - TI);
+              }
+            }
 #pragma unroll
             for (int j = 0; j < TJ; ++j)
               acc[i][j] = mma(fa[ks & 1][i], fb[ks & 1][j], acc[i][j]);
