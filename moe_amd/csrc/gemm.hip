@@ -724,7 +724,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
         WAIT_VMCNT_LGKM0(CPW);
       }
       __builtin_amdgcn_s_barrier();  // B(0)
-      tok_offsets(2, tk_a);  // its load is older than stage 0's DMA
+      tok_offsets(2, tk_a);  // its load precedes stage 0's row half, which B(0) waited for
       slot_bases(0, (uint32_t)SLOT);
 #pragma unroll
       for (int i = 0; i < TI; ++i) fa[0][i] = read_a(0, i);
@@ -764,6 +764,9 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
             for (int j = 0; j < TJ; ++j)
               acc[i][j] = mma(fa[ks & 1][i], fb[ks & 1][j], acc[i][j]);
             group_order();
+            // Scalar instructions (slot offsets, descriptors, M0) may cross
+            // the group boundaries; memory ops keep the issue order that the
+            // wait counts rely on.
             __builtin_amdgcn_sched_barrier(0x4);
           }
         }
