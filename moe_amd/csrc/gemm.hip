@@ -242,6 +242,15 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
   constexpr int CPW = BC * BK * 2 / 1024 / NW;            // 1 KB DMA blocks per wave, column half
   constexpr int RPW = BR * BK * 2 / 1024 / NW;            // ... row half
   constexpr int NTOK = GCOL ? 1 : 0;                      // gathered-row index loads per stage
+  // Ring order: each stage's first half (ring position 2s) is issued a stage
+  // before its second half (2s+1), so it has about 1.5 stages of lead to the
+  // barrier that needs it, the second half about one.  The row half goes
+  // first where that measured faster (G1F's gathered token rows: -1.5% at L;
+  // G1DX -0.8%; the dense mode), the column half elsewhere (G2F +3% with the
+  // rows first).  The dW GEMMs keep the column half first: their row_src
+  // pipeline fetches the gathered column operand's entries a stage ahead.
+  constexpr bool ROW_FIRST = MODE == G1F || MODE == G1DX || MODE == RL;
+  constexpr int FPW = ROW_FIRST ? RPW : CPW, SPW = ROW_FIRST ? CPW : RPW;  // DMA ops per half
   constexpr int NOPS = NTOK + RPW + CPW;                  // memory ops per main-loop step
   constexpr int NGRP = (BK / 16) * TI;                    // MFMA groups per step
   static_assert(CPW * NW == 32 && RPW * NW * 8 == BR && TJ >= 1, "DMA blocks per wave");
@@ -250,7 +259,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
   constexpr bool PF = MODE == G1F || MODE == G2F || MODE == G1DX || MODE == G1DW || MODE == G2DWG ||
                       MODE == RDX;
   constexpr int NST = (MODE == G1F ? 12 : 8) * TJ;
-  static_assert(!PF || CPW + NST <= 63, "vmcnt range");
+  static_assert(!PF || FPW + NST <= 63, "vmcnt range");
   static_assert(TOKEN || DENSE || BR == 256, "dW modes use 256-row tiles");
 
   extern __shared__ __attribute__((aligned(16))) bf16 smem[];
@@ -562,14 +571,14 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
     }
   };
   auto issue_col = [&](int s, const int (&tk)[NTOK > 0 ? NTOK : 1]) {
-    char* base = slot_ptr(2 * s);
+    char* base = slot_ptr(2 * s + (ROW_FIRST ? 1 : 0));
     const auto rs = stage_rsrc(cptr, cbytes, kst(s) * cstep, s);
 #pragma unroll
     for (int i = 0; i < CPW; ++i) dma16(rs, col_off(s, i, tk), base + (wid + NW * i) * 1024);
   };
-  // DMA of the row half of stage s (ring position 2s+1).
+  // DMA of the row half of stage s (ring position 2s+1, or 2s if ROW_FIRST).
   auto issue_row = [&](int s) {
-    char* base = slot_ptr(2 * s + 1);
+    char* base = slot_ptr(2 * s + (ROW_FIRST ? 0 : 1));
     const auto rs = stage_rsrc(rptr, rbytes, kst(s) * rstep, s);
 #pragma unroll
     for (int i = 0; i < RPW; ++i) dma16(rs, roff[i], base + (wid + NW * i) * 1024);
@@ -655,13 +664,16 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       fetch_tok(0, tk_a);
       fetch_tok(1, tk_b);
       tok_offsets(0, tk_a);
-      issue_col(0, tk_a);
+      if constexpr (ROW_FIRST) issue_row(0);
+      else issue_col(0, tk_a);
       __builtin_amdgcn_sched_barrier(0);
       fetch_tok(2, tk_a);
-      issue_row(0);
+      if constexpr (ROW_FIRST) issue_col(0, tk_a);
+      else issue_row(0);
       __builtin_amdgcn_sched_barrier(0);
       tok_offsets(1, tk_b);
-      issue_col(1, tk_b);
+      if constexpr (ROW_FIRST) issue_row(1);
+      else issue_col(1, tk_b);
       if constexpr (MODE == G2DXF) {
         // The row's routing weight, in flight under the main loop (raw bits:
         // converting here would wait for the load).  Being the youngest op,
@@ -680,26 +692,31 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       // positions advance by two per stage, so the five offsets rotate by
       // two at the end of each stage (register moves, not a modulo).
       uint32_t rq[5] = {0, SLOT, 2 * SLOT, 3 * SLOT, 4 * SLOT};
-      // Op o of window W(w): its row half (stage w+1, descriptor rsr) lands at
-      // ring offset srow, its column half (stage w+2, descriptor rsc) at
-      // scol; `tk` holds the row_src entries of stage w+2.  A window begins
-      // in the last sub-step of the stage before, so its row descriptor is
-      // formed once there and carried into the next iteration.
-      static_assert(TI * NOPS / NGRP <= NTOK + RPW, "a window's first TI groups hold no column op");
+      // Op o of window W(w): the second half of stage w+1 (descriptor rsr)
+      // lands at ring offset srow, the first half of stage w+2 (descriptor
+      // rsc) at scol; `tk` holds the row_src entries of stage w+2.  A window
+      // begins in the last sub-step of the stage before, so its second-half
+      // descriptor is formed once there and carried into the next iteration.
+      static_assert(TI * NOPS / NGRP <= NTOK + SPW, "a window's first TI groups hold no first-half op");
       auto row_rsrc = [&](int s) { return stage_rsrc(rptr, rbytes, kst(s) * rstep, s); };
       auto col_rsrc = [&](int s) { return stage_rsrc(cptr, cbytes, kst(s) * cstep, s); };
+      // descriptors of the second half of stage s and the first half of stage s
+      auto second_rsrc = [&](int s) { return ROW_FIRST ? col_rsrc(s) : row_rsrc(s); };
+      auto first_rsrc = [&](int s) { return ROW_FIRST ? row_rsrc(s) : col_rsrc(s); };
       auto win_op = [&](int w, int o, const int (&tk)[NTOK > 0 ? NTOK : 1], uint32_t srow,
                         uint32_t scol, __amdgpu_buffer_rsrc_t rsr, __amdgpu_buffer_rsrc_t rsc) {
         if (o < NTOK) {
           if constexpr (GCOL)
             tn[0] = __builtin_amdgcn_raw_buffer_load_b32(
                 isrc, (uint32_t)(kb_cur + (w + 3) * BK + lane) * 4, 0, 0);
-        } else if (o < NTOK + RPW) {
+        } else if (o < NTOK + SPW) {  // second half of stage w+1, at srow with rsr
           const int i = o - NTOK;
-          dma16(rsr, roff[i], (char*)smem + srow + (wid + NW * i) * 1024);
-        } else {
-          const int i = o - NTOK - RPW;
-          dma16(rsc, col_off(w + 2, i, tk), (char*)smem + scol + (wid + NW * i) * 1024);
+          if constexpr (ROW_FIRST) dma16(rsr, col_off(w + 1, i, tk), (char*)smem + srow + (wid + NW * i) * 1024);
+          else dma16(rsr, roff[i], (char*)smem + srow + (wid + NW * i) * 1024);
+        } else {  // first half of stage w+2, at scol with rsc
+          const int i = o - NTOK - SPW;
+          if constexpr (ROW_FIRST) dma16(rsc, roff[i], (char*)smem + scol + (wid + NW * i) * 1024);
+          else dma16(rsc, col_off(w + 2, i, tk), (char*)smem + scol + (wid + NW * i) * 1024);
         }
       };
       // Issue order inside an MFMA group: two MFMAs, the group's memory
@@ -718,27 +735,27 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       if constexpr (PF) {
         // the previous tile's NST epilogue stores were issued after this
         // tile's first stages: they may still be in flight
-        if (after_epi) WAIT_VMCNT_LGKM0(CPW + NST);
-        else WAIT_VMCNT_LGKM0(CPW);
+        if (after_epi) WAIT_VMCNT_LGKM0(FPW + NST);
+        else WAIT_VMCNT_LGKM0(FPW);
       } else {
-        WAIT_VMCNT_LGKM0(CPW);
+        WAIT_VMCNT_LGKM0(FPW);
       }
       __builtin_amdgcn_s_barrier();  // B(0)
       tok_offsets(2, tk_a);  // its load precedes stage 0's row half, which B(0) waited for
-      slot_bases(0, (uint32_t)SLOT);
+      slot_bases(ROW_FIRST ? (uint32_t)SLOT : 0u, ROW_FIRST ? 0u : (uint32_t)SLOT);
 #pragma unroll
       for (int i = 0; i < TI; ++i) fa[0][i] = read_a(0, i);
 #pragma unroll
       for (int j = 0; j < TJ; ++j) fb[0][j] = read_b(0, j);
       // the part of W(0) that belongs to the (absent) last sub-step of stage -1
-      __amdgpu_buffer_rsrc_t rs_row = row_rsrc(1);  // W(0)'s row half: stage 1
+      __amdgpu_buffer_rsrc_t rs_second = second_rsrc(1);  // W(0)'s second half: stage 1
 #pragma unroll
       for (int o = 0; o < TI * NOPS / NGRP; ++o) {
-        win_op(0, o, tk_a, rq[3], rq[4], rs_row, rs_row);  // ring positions 3 and 4 (no column op)
+        win_op(0, o, tk_a, rq[3], rq[4], rs_second, rs_second);  // ring positions 3 and 4 (no first-half op)
         __builtin_amdgcn_sched_barrier(0);
       }
       for (int kt = 0; kt < cur.nk; ++kt) {
-        const __amdgpu_buffer_rsrc_t rs_col = col_rsrc(kt + 2);
+        const __amdgpu_buffer_rsrc_t rs_first = first_rsrc(kt + 2);
         // Sub-steps 0..2 of stage kt; groups TI..NGRP-1 of W(kt).
 #pragma unroll
         for (int ks = 0; ks < GQ; ++ks) {
@@ -747,7 +764,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
             const int q = TI + ks * TI + i;
 #pragma unroll
             for (int o = q * NOPS / NGRP; o < (q + 1) * NOPS / NGRP; ++o)
-              win_op(kt, o, tk_a, rq[3], rq[4], rs_row, rs_col);  // positions 2kt+3, 2kt+4
+              win_op(kt, o, tk_a, rq[3], rq[4], rs_second, rs_first);  // positions 2kt+3, 2kt+4
             if (ks + 1 < GQ) {
               fa[(ks + 1) & 1][i] = read_a(ks + 1, i);
               if (i < TJ) fb[(ks + 1) & 1][i] = read_b(ks + 1, i);
@@ -781,17 +798,18 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
         // barrier lets other waves overwrite their slots.  (After the last
         // stage this barrier, the reads of the stage past it and the ops of
         // the window after it are junk, kept to make every iteration alike.)
-        WAIT_VMCNT_LGKM0(CPW);
+        WAIT_VMCNT_LGKM0(FPW);
         __builtin_amdgcn_s_barrier();  // B(kt+1)
-        slot_bases(rq[2], rq[3]);  // stage kt+1: positions 2kt+2, 2kt+3
+        // stage kt+1: first half at position 2kt+2, second half at 2kt+3
+        slot_bases(ROW_FIRST ? rq[3] : rq[2], ROW_FIRST ? rq[2] : rq[3]);
         // Last sub-step of stage kt, groups 0..TI-1 of W(kt+1), and the
         // fragments of sub-step 0 of stage kt+1.
-        rs_row = row_rsrc(kt + 2);
+        rs_second = second_rsrc(kt + 2);
 #pragma unroll
         for (int i = 0; i < TI; ++i) {
 #pragma unroll
           for (int o = i * NOPS / NGRP; o < (i + 1) * NOPS / NGRP; ++o)
-            win_op(kt + 1, o, tk_a, rq[0], rq[1], rs_row, rs_row);  // positions 2kt+5, 2kt+6
+            win_op(kt + 1, o, tk_a, rq[0], rq[1], rs_second, rs_second);  // positions 2kt+5, 2kt+6
           fa[0][i] = read_a(0, i);
           if (i < TJ) fb[0][i] = read_b(0, i);
 #pragma unroll
@@ -988,16 +1006,17 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
     // --------------------------------------------------------- main loop
-    // Ring position h holds the column half (h = 2s) or the row half
-    // (h = 2s+1) of stage s, in slot h % 5.  Barrier B(s) comes after each
-    // wave has waited until only the last-issued column half (stage s+1)
-    // may still be in flight: stage s has landed everywhere, and every wave
+    // Ring position h holds the first half (h = 2s: the column half, or the
+    // row half where ROW_FIRST) or the second half (h = 2s+1) of stage s, in
+    // slot h % 5.  Barrier B(s) comes after each wave has waited until only
+    // the last-issued first half (stage s+1) may still be in flight: stage
+    // s has landed everywhere, and every wave
     // has finished reading stage s-1.  B(s+1) sits before the last k
     // sub-step of stage s (whose fragments are already in registers), so
     // that the first fragments of stage s+1 are read while those MFMAs run.
     // Window W(s), the memory ops issued after B(s), is: the row_src
-    // entries of stage s+3 (G1DW), the DMA of the row half of stage s+1 and
-    // of the column half of stage s+2 (into stage s-1's slots), in this
+    // entries of stage s+3 (G1DW), the DMA of the second half of stage s+1
+    // and of the first half of stage s+2 (into stage s-1's slots), in this
     // order, spread over 16 MFMA groups (the last sub-step of stage s-1 and
     // the first three of stage s): issued in one burst they back up the
     // texture pipe and stall MFMA issue.  Stages past the last one are
