@@ -249,15 +249,15 @@ def copy_calibration(nbytes: int) -> None:
 # in profiles/gemm_hbm_traffic_L.md and profiles/retrofit_hbm_traffic.md.
 RECORDED_TRAFFIC = {
     "L": {
-        "gemm_gate_up_swiglu": 10872190451,
-        "gemm_down": 4706852918,
-        "gemm_down_backward_dx_fused": 8048345657,
-        "gemm_down_backward_dw_gathered": 4559195489,
-        "gemm_gate_up_backward_dx": 8378161604,
-        "gemm_gate_up_backward_dw": 6909547531,
-        "torch_gating_linear": 289695900,
-        "router_linear_backward_dx": 290691587,
-        "router_linear_backward_dw": 318965935,
+        "gemm_gate_up_swiglu": 11949127500,
+        "gemm_down": 4769979673,
+        "gemm_down_backward_dx_fused": 8035119201,
+        "gemm_down_backward_dw_gathered": 4583216077,
+        "gemm_gate_up_backward_dx": 8521477011,
+        "gemm_gate_up_backward_dw": 6890277298,
+        "torch_gating_linear": 289704819,
+        "router_linear_backward_dx": 290830219,
+        "router_linear_backward_dw": 318973843,
     },
     "Retrofit": {
         "gemm_gate_up_backward_dw": 12607157703,
