@@ -723,11 +723,26 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       // ops, one MFMA, its fragment reads, the last MFMA (measured best
       // among the orders tried).
       auto group_order = [&]() {
-        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
-        __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);  // VMEM read (the group's 0-2 ops)
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // DS read (2-4 fragment reads)
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if constexpr (MODE == G1F) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);  // VMEM read (the group's 0-2 ops)
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // DS read (2-4 fragment reads)
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        } else {
+          // the same, with up to five scalar instructions placed after each
+          // of the first three MFMAs (dW GEMMs -1 to -2%, G2F -0.7%; G1F
+          // measured no better)
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x004, 5, 0);  // SALU
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);  // VMEM read
+          __builtin_amdgcn_sched_group_barrier(0x004, 5, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // DS read
+          __builtin_amdgcn_sched_group_barrier(0x004, 5, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        }
       };
       constexpr int GQ = BK / 16 - 1;  // groups before the last sub-step: NGRP - TI
       constexpr int NLR = TI + TJ;     // fragment reads of a sub-step
