@@ -249,15 +249,15 @@ def copy_calibration(nbytes: int) -> None:
 # in profiles/gemm_hbm_traffic_L.md and profiles/retrofit_hbm_traffic.md.
 RECORDED_TRAFFIC = {
     "L": {
-        "gemm_gate_up_swiglu": 11949127500,
-        "gemm_down": 4769979673,
-        "gemm_down_backward_dx_fused": 8035119201,
-        "gemm_down_backward_dw_gathered": 4583216077,
-        "gemm_gate_up_backward_dx": 8521477011,
-        "gemm_gate_up_backward_dw": 6890277298,
-        "torch_gating_linear": 289704819,
-        "router_linear_backward_dx": 290830219,
-        "router_linear_backward_dw": 318973843,
+        "gemm_gate_up_swiglu": 11617452787,
+        "gemm_down": 4745965057,
+        "gemm_down_backward_dx_fused": 7814923499,
+        "gemm_down_backward_dw_gathered": 4626583699,
+        "gemm_gate_up_backward_dx": 8857669989,
+        "gemm_gate_up_backward_dw": 7192684761,
+        "torch_gating_linear": 289694449,
+        "router_linear_backward_dx": 290641825,
+        "router_linear_backward_dw": 318965858,
     },
     "Retrofit": {
         "gemm_gate_up_backward_dw": 12607157703,
