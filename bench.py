@@ -174,6 +174,36 @@ def routing_gating_check(cfg, x, wr, inp) -> dict:
             "hip_gating_logits_differing": logit_diff}
 
 
+def routing_vs_torch_topk(cfg, x, wr, inp, gating: str, idx) -> dict:
+    """Outside the timed steps: the timed step's routing `idx` against the
+    reference's own selection on this device -- torch.softmax(logits, fp32)
+    then torch.topk (src/models/modeling_qwen3_moe.py:269-270), or
+    torch.sigmoid then torch.topk(scores + expert_bias) (src/models/
+    router.py:112-127) -- on the logits of the timed gating source."""
+    from moe_amd import library
+    sig = cfg.router == "sigmoid"
+    with torch.no_grad():
+        logits = library.gating_logits(x.detach(), wr.detach(), gating, fp32=sig)
+        if sig:
+            ref = torch.sigmoid(logits) + inp.expert_bias
+        else:
+            z = logits if inp.logit_offset is None else logits.float() + inp.logit_offset
+            ref = torch.softmax(z, dim=-1, dtype=torch.float32)
+        tv, ti = torch.topk(ref, cfg.K, dim=-1)
+        set_diff = (idx.sort(dim=1).values != ti.sort(dim=1).values).any(dim=1)
+        pos_diff = idx != ti
+        unequal = (pos_diff & (ref.gather(1, idx) != tv)).any(dim=1)
+        counts_eq = torch.equal(torch.bincount(idx.reshape(-1), minlength=cfg.E),
+                                torch.bincount(ti.reshape(-1), minlength=cfg.E))
+    return {"reference_selection": "torch.topk on the device, on torch."
+                                   + ("sigmoid(logits) + expert_bias" if sig
+                                      else "softmax(logits, fp32)"),
+            "topk_set_mismatch": int(set_diff.sum()),
+            "topk_order_only_differences": int((pos_diff.any(dim=1) & ~set_diff).sum()),
+            "order_differences_between_unequal_values": int(unequal.sum()),
+            "per_expert_counts_equal": bool(counts_eq)}
+
+
 def _event_ms(fn, reps: int) -> float:
     """Mean HIP-event time of fn() on torch's current stream (2 warm-up calls)."""
     for _ in range(2):
@@ -514,8 +544,10 @@ def main():
         "kernels": kernels,
         "routing": dict(routing_gating_check(cfg, x, wr, inp),
                         timed_gating=args.gating,
-                        timed_routing="bit-identical to the reference's (torch F.linear logits)"
-                        if args.gating == "torch" else "MFMA gating logits"),
+                        timed_logits="torch F.linear: bit-identical to the reference's"
+                        if args.gating == "torch" else "MFMA gating kernel",
+                        timed_step_vs_reference=routing_vs_torch_topk(cfg, x, wr, inp,
+                                                                      args.gating, idx)),
     }
     if cfg.router == "softmax" and cfg.backward:
         result["routing_consumers"] = routing_consumers(cfg, probs_for_consumers(cfg, x, wr, inp),

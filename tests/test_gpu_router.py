@@ -104,28 +104,16 @@ def test_sigmoid_router_parity(T, H, E, K, groups, gtk, sf, wdt):
     tpe = torch.zeros(E, device=DEV)
     scores, w, idx = ops.router_sigmoid_topk(logits, bias, K, True, sf, groups, gtk, wdt, tpe)
     torch.cuda.synchronize()
-    s_ref = torch.sigmoid(logits.cpu())
-    assert torch.allclose(scores.cpu(), s_ref, rtol=2e-6, atol=1e-7)
-    # Selection parity on the kernel's own scores is exact; against the
-    # oracle's scores it is exact except where a 1-ulp sigmoid difference
-    # can reorder a near-tie, which is checked explicitly.
-    sc = scores.cpu()
-    if groups is None:
-        _, i_own = O.rank_topk(sc + bias.cpu(), K)
-    else:
-        _, i_own = O.group_limited_topk(sc + bias.cpu(), K, groups, gtk)
-    assert torch.equal(idx.cpu(), i_own), "selection on the kernel's scores differs"
-    _, w_ref, i_ref = O.sigmoid_router(logits.cpu(), bias.cpu(), K, True, sf, groups, gtk, wdt)
-    bad = (idx.cpu() != i_ref).any(-1).nonzero().flatten()
-    biased = s_ref + bias.cpu()
-    for t in bad.tolist():
-        row = biased[t].sort(descending=True).values
-        gaps = (row[:-1] - row[1:])[: K + 1]
-        assert gaps.min() < 1e-6, f"token {t}: index mismatch without a near-tie"
-    assert bad.numel() <= max(2, T // 1000)
-    ok = torch.ones(T, dtype=torch.bool)
-    ok[bad] = False
-    assert torch.allclose(w.cpu()[ok].float(), w_ref[ok].float(), rtol=1e-5 if wdt == torch.float32
+    # The scores are torch.sigmoid's on this device bit for bit (the
+    # reference's call, router.py:112); selection and weights are then
+    # exact against the oracle on those scores.
+    s_dev = torch.sigmoid(logits)
+    assert torch.equal(scores, s_dev), "scores differ from torch.sigmoid on the device"
+    sc = s_dev.cpu()
+    assert torch.allclose(sc, torch.sigmoid(logits.cpu()), rtol=2e-6, atol=1e-7)
+    w_ref, i_ref = O.sigmoid_router_from_scores(sc, bias.cpu(), K, True, sf, groups, gtk, wdt)
+    assert torch.equal(idx.cpu(), i_ref), "selection differs from the oracle's"
+    assert torch.allclose(w.cpu().float(), w_ref.float(), rtol=1e-5 if wdt == torch.float32
                           else 8e-3, atol=1e-7)
     counts = torch.bincount(idx.cpu().reshape(-1), minlength=E).float()
     assert torch.equal(tpe.cpu(), counts)
