@@ -82,6 +82,25 @@ int moe_amd_router_linear_softmax_topk(const void* hidden_states, const void* we
                                        int renormalize, float* probs, float* topk_weights,
                                        int64_t* topk_index, void* logits, void* stream);
 
+/* The gating linear with the DeepSeek-V3 router fused into its epilogue:
+ * scores[T,E] fp32, topk_weights[T,K] (weights_dtype) and topk_index[T,K]
+ * int64 exactly as moe_amd_router_linear (fp32 logits) followed by
+ * moe_amd_router_sigmoid_topk with the same arguments (same logits, same
+ * selection and weight arithmetic, bit for bit), without the fp32 logits'
+ * round trip through memory; the fp32 logits are also written when `logits`
+ * is not NULL, and tokens_per_expert (may be NULL) accumulates the
+ * selection counts.  Replaces F.linear(h.float(), W.float()), sigmoid,
+ * biased (group-limited) top-K, renormalisation and scaling of
+ * DeepSeekRouter.forward (src/models/router.py:107-152; group_limited_topk
+ * :22-70).  Shapes: H multiple of 64, E multiple of 8 with E <= 128, K <= 8,
+ * num_groups 0 (flat) or at most 8 (else MOE_ERR_UNSUPPORTED). */
+int moe_amd_router_linear_sigmoid_topk(const void* hidden_states, const void* weight, int64_t T,
+                                       int E, int H, const float* expert_bias, int K,
+                                       int renormalize, float scaling_factor, int num_groups,
+                                       int group_topk, float* scores, void* topk_weights,
+                                       int weights_dtype, int64_t* topk_index,
+                                       float* tokens_per_expert, float* logits, void* stream);
+
 /* The gating linear's input gradient for bf16 logits: d_x[T,H] =
  * bf16(d_logits[T,E] . weight[E,H]) (bf16 inputs, fp32 accumulation) -- the
  * grad_input of F.linear's backward (autograd of

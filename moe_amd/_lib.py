@@ -39,6 +39,8 @@ SIGNATURES: dict[str, tuple] = {
     "moe_amd_router_linear": (_i, [_p, _p, _i64, _i, _i, _p, _i, _p]),
     "moe_amd_router_linear_softmax_topk": (
         _i, [_p, _p, _i64, _i, _i, _p, _i, _i, _p, _p, _p, _p, _p]),
+    "moe_amd_router_linear_sigmoid_topk": (
+        _i, [_p, _p, _i64, _i, _i, _p, _i, _i, _f, _i, _i, _p, _p, _i, _p, _p, _p, _p]),
     "moe_amd_router_linear_backward_dx": (_i, [_p, _p, _i64, _i, _i, _p, _p]),
     "moe_amd_router_linear_backward_dw_workspace_size": (_sz, [_i64, _i, _i]),
     "moe_amd_router_linear_backward_dw": (_i, [_p, _p, _i64, _i, _i, _p, _sz, _p, _p]),

@@ -81,6 +81,9 @@ constexpr int SROW = 260;  // bf16 per row of the epilogue staging tile (520 B: 
 // RDX: its input gradient, d_x[T, H] = d_logits[T, E] . W_r[E, H].
 // RLTK: RLT with the softmax router fused into its epilogue (probs, top-K
 //      weights and ids written from the bf16 logits of the staging tile).
+// RLTS: RLT with the DeepSeek router fused into its epilogue (fp32 logits
+//      staged, sigmoid scores, biased and optionally group-limited top-K,
+//      renormalised and scaled weights, selection counts).
 // RLT: the same logits computed transposed, rows = experts (W_r, at most one
 //      or two row tiles) and columns = tokens, with the MFMA operands
 //      swapped so that the tile is stored as logits[T, E]: for E <= 128 a
@@ -94,7 +97,7 @@ constexpr int SROW = 260;  // bf16 per row of the epilogue staging tile (520 B: 
 // computes d_down_proj[e]^T = (w act)^T d_out[tokens] and stores it
 // transposed.
 enum Mode { G1F = 0, G2F = 1, G2DX = 2, G1DX = 3, G2DW = 4, G1DW = 5, RL = 6, RDX = 7, RDW = 8,
-            G2DXF = 9, G2DWG = 10, RLT = 11, RLTK = 12 };
+            G2DXF = 9, G2DWG = 10, RLT = 11, RLTK = 12, RLTS = 13 };
 
 struct GemmArgs {
   const bf16* x;         // hidden_states [T,H]
@@ -120,10 +123,14 @@ struct GemmArgs {
   int tok_shift;         // 31 + ceil(log2(topk))
   int n_ct, n_rt, n_tiles;  // n_tiles: dW modes (host-known)
   float* probs;          // RLTK: router outputs probs [T,E] fp32, top-K weights [T,K] fp32,
-  float* topk_w;         //   top-K ids [T,K] int64; logit offset [E] (may be null)
-  int64_t* topk_idx;
-  const float* offset;
+  float* topk_w;         //   top-K ids [T,K] int64; logit offset [E] (may be null).
+  int64_t* topk_idx;     //   RLTS: scores [T,E] fp32 in probs, weights [T,K] (bf16 if
+  const float* offset;   //   w_bf16) in topk_w, fp32 logits in out_f32 (may be null)
   int renorm;
+  const float* bias;     // RLTS: expert_bias [E] (may be null), scaling factor (0: none),
+  float scaling;         //   expert groups (0: flat top-K) and groups kept, counts [E]
+  int ngroups, gtopk, w_bf16;  // (may be null)
+  float* tpe;
   int* queue;            // G2DW/G1DW: this GEMM's 8 XCD tile counters + finished count (null: static walk)
   const int* xstart;     // ... experts of XCD x: xorder[xstart[x] .. xstart[x+1])
   const int* xorder;
@@ -223,7 +230,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
   constexpr int NW = kWaves<BR>;                          // waves, as NW/2 rows x 2 columns
   constexpr int NTHR = NW * 64;
   constexpr bool TOKEN = MODE <= G1DX || MODE == G2DXF;   // rows = routed rows of one expert
-  constexpr bool TRL = MODE == RLT || MODE == RLTK;        // transposed router linear
+  constexpr bool TRL = MODE == RLT || MODE == RLTK || MODE == RLTS;  // transposed router linear
   if constexpr (TOKEN) {
     constexpr int my_tile = BR == 64 ? 0 : (BR == 128 ? 1 : 2);
     if (p.row_tile && __builtin_amdgcn_readfirstlane(*p.row_tile) != my_tile) return;
@@ -975,6 +982,13 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       }
     }
   };
+  // RLTS: the selection counts of this lane's experts (entries e0 .. e0+SV-1
+  // of its lane group of 8), summed over every token it routes and flushed
+  // to the counts once, after the last tile.
+  constexpr int SV = MODE == RLTS ? BR / 8 : 1;
+  int scnt[SV];
+#pragma unroll
+  for (int j = 0; j < SV; ++j) scnt[j] = 0;
   if constexpr (PF) {
     // (a dynamic walk may find no tile at all; every workgroup still
     // reaches the finished-count update below)
@@ -1044,6 +1058,82 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
 
     // --------------------------------------------------------- epilogue
     WAIT_VMCNT(0);    // no LDS DMA may still be landing in the stages
+    if constexpr (MODE == RLTS) {
+      // The DeepSeek router fused into the gating linear.  The fp32 logits
+      // of BC tokens x BR experts are staged as [token][expert] (rows of
+      // BR + 4 floats); 8 lanes per token then take sigmoid scores, rank
+      // keys of the biased scores and the selection (router_group.h) --
+      // the arithmetic of router_linear with fp32 logits followed by
+      // router_sigmoid_topk, bit for bit -- and write the scores, the
+      // top-K weights and ids, and (if asked) the logits.
+      constexpr int G = 8, V = SV, TPP = NTHR / G, FROW = BR + 4;
+      __syncthreads();  // every wave is done reading the k-stages
+      float* const stf = (float*)smem;
+#pragma unroll
+      for (int j = 0; j < TJ; ++j)
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int tokl = wc * 128 + i * 32 + l32;
+            const int el = wr * WR + j * 32 + 8 * q + 4 * hl;
+            *(f32x4*)(stf + tokl * FROW + el) =
+                f32x4{acc[i][j][4 * q + 0], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                      acc[i][j][4 * q + 3]};
+          }
+      __syncthreads();
+      const int g = tid & (G - 1), e0 = g * V;
+      const int E = p.E, K = p.topk;
+      float bv[V];
+      int grp[V];
+      const int eg = p.ngroups > 0 ? E / p.ngroups : 1;
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        const int e = e0 + j;
+        bv[j] = (p.bias && e < E) ? p.bias[e] : 0.f;
+        grp[j] = e < E ? e / eg : -1;
+      }
+      for (int rr = tid / G; rr < BC; rr += TPP) {
+        const int64_t t = (int64_t)cur.ct * BC + rr;
+        const bool tok = t < p.T;
+        float lg[V], sc[V];
+        uint64_t key[V];
+#pragma unroll
+        for (int q = 0; q < V / 4; ++q) {
+          const f32x4 a = *(const f32x4*)(stf + rr * FROW + e0 + 4 * q);
+#pragma unroll
+          for (int h = 0; h < 4; ++h) lg[4 * q + h] = a[h];
+        }
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+          const int e = e0 + j;
+          sc[j] = e < E ? dsk_score(lg[j], 0) : 0.f;
+          key[j] = e < E ? rank_key(sc[j] + bv[j], e) : 0ull;
+        }
+        float my_w;
+        int my_e;
+        group_sigmoid_topk<G, V>(sc, key, grp, g, K, p.ngroups, p.gtopk, p.renorm, p.scaling,
+                                 tok && p.tpe != nullptr, scnt, my_w, my_e);
+        if (tok) {
+#pragma unroll
+          for (int q = 0; q < V / 4; ++q)
+            if (e0 + 4 * q < E) {
+              *(f32x4*)(p.probs + t * E + e0 + 4 * q) =
+                  f32x4{sc[4 * q], sc[4 * q + 1], sc[4 * q + 2], sc[4 * q + 3]};
+              if (p.out_f32)
+                *(f32x4*)(p.out_f32 + t * E + e0 + 4 * q) =
+                    f32x4{lg[4 * q], lg[4 * q + 1], lg[4 * q + 2], lg[4 * q + 3]};
+            }
+          if (g < K) {
+            if (p.w_bf16) ((bf16*)p.topk_w)[t * K + g] = f2bf(my_w);
+            else p.topk_w[t * K + g] = my_w;
+            p.topk_idx[t * K + g] = my_e;
+          }
+        }
+      }
+      __syncthreads();  // staging reads done before the next tile's stages land
+      continue;
+    }
     if constexpr (MODE == RLT) {
       if (p.out_f32) {
         // fp32 logits: with the operands swapped each lane holds 4
@@ -1362,6 +1452,22 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
     __syncthreads();  // staging reads done before the next tile's stages land
   }
   }
+  if constexpr (MODE == RLTS) {
+    // Selection counts: the lanes' counts summed per expert in LDS (free:
+    // the last tile ended with a barrier), then one atomic add per expert.
+    if (p.tpe) {
+      int* const hist = (int*)smem;
+      for (int e = tid; e < p.E; e += NTHR) hist[e] = 0;
+      __syncthreads();
+      const int e0 = (tid & 7) * SV;
+#pragma unroll
+      for (int j = 0; j < SV; ++j)
+        if (scnt[j] && e0 + j < p.E) atomicAdd(&hist[e0 + j], scnt[j]);
+      __syncthreads();
+      for (int e = tid; e < p.E; e += NTHR)
+        if (hist[e]) atomicAdd(&p.tpe[e], (float)hist[e]);
+    }
+  }
   if (dyn && tid == 0) {
     // The last workgroup to finish resets the counters for the next launch.
     const int d = __hip_atomic_fetch_add(p.queue + 8, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1399,8 +1505,11 @@ int launch(const GemmArgs& a, int max_tiles, hipStream_t st) {
   constexpr size_t stages = (size_t)NSLOT * SLOT;
   // staging tile ([BC][SROW] when transposed), plus G2DXF's per-row weights
   // and row_src
-  constexpr size_t staging = (size_t)((MODE == G2DWG || MODE == RLT || MODE == RLTK) ? BC : BR) * SROW * sizeof(bf16) +
-                             (MODE == G2DXF ? (size_t)BR * 8 : 0);
+  constexpr size_t staging =
+      MODE == RLTS ? (size_t)BC * (BR + 4) * sizeof(float)  // fp32 logits [token][expert]
+                   : (size_t)((MODE == G2DWG || MODE == RLT || MODE == RLTK) ? BC : BR) * SROW *
+                             sizeof(bf16) +
+                         (MODE == G2DXF ? (size_t)BR * 8 : 0);
   const size_t lds = stages > staging ? stages : staging;
   if (max_tiles <= 0) return MOE_OK;
   hipError_t err = hipFuncSetAttribute((const void*)grouped_gemm_kernel<MODE, BR>,
@@ -1629,6 +1738,62 @@ extern "C" int moe_amd_router_linear_softmax_topk(const void* hidden_states, con
   a.n_tiles = a.n_ct;
   if (g8) return launch<RLTK, 128>(a, a.n_tiles, (hipStream_t)stream);
   return launch<RLTK, 256>(a, a.n_tiles, (hipStream_t)stream);
+}
+
+extern "C" int moe_amd_router_linear_sigmoid_topk(
+    const void* hidden_states, const void* weight, int64_t T, int E, int H,
+    const float* expert_bias, int K, int renormalize, float scaling_factor, int num_groups,
+    int group_topk, float* scores, void* topk_weights, int weights_dtype, int64_t* topk_index,
+    float* tokens_per_expert, float* logits, void* stream) {
+  const char* who = "router_linear_sigmoid_topk";
+  MOE_REQUIRE(T >= 0 && E >= 1 && H > 0 && K >= 1 && K <= E, MOE_ERR_ARG, "%s: bad sizes", who);
+  MOE_REQUIRE(H % 64 == 0 && E % 8 == 0, MOE_ERR_ARG,
+              "%s: H=%d must be a multiple of 64 and E=%d of 8", who, H, E);
+  // The fused epilogue ranks with 8 lanes per token (K <= 8) and 8 or 16
+  // experts per lane (E <= 128), expert groups one lane's score each.
+  MOE_REQUIRE(E <= 128 && K <= 8, MOE_ERR_UNSUPPORTED,
+              "%s: E=%d, K=%d outside the fused shapes (E <= 128, K <= 8); use "
+              "moe_amd_router_linear + moe_amd_router_sigmoid_topk", who, E, K);
+  if (num_groups > 0) {
+    MOE_REQUIRE(num_groups <= 8 && E % num_groups == 0 && group_topk >= 1 &&
+                    group_topk <= num_groups && K % group_topk == 0 &&
+                    (E / num_groups) * group_topk >= K,
+                MOE_ERR_ARG, "%s: bad grouping (E=%d K=%d groups=%d group_topk=%d; the fused "
+                "form takes at most 8 groups)", who, E, K, num_groups, group_topk);
+  }
+  MOE_REQUIRE(weights_dtype == MOE_DTYPE_F32 || weights_dtype == MOE_DTYPE_BF16, MOE_ERR_DTYPE,
+              "%s: weights dtype %d", who, weights_dtype);
+  MOE_REQUIRE(weight && (T == 0 || (hidden_states && scores && topk_weights && topk_index)),
+              MOE_ERR_ARG, "%s: null pointer", who);
+  MOE_ALIGNED(hidden_states, who);
+  MOE_ALIGNED(weight, who);
+  MOE_ALIGNED(scores, who);
+  MOE_ALIGNED(logits, who);
+  MOE_REQUIRE(T * (int64_t)H * 2 < ((int64_t)1 << 31) && (int64_t)E * H * 2 < ((int64_t)1 << 31),
+              MOE_ERR_UNSUPPORTED, "%s: T*H or E*H too large for 32-bit offsets", who);
+  if (T == 0) return MOE_OK;
+  GemmArgs a{};
+  a.x = (const bf16*)hidden_states;
+  a.a0 = (const bf16*)weight;
+  a.probs = scores;
+  a.topk_w = (float*)topk_weights;
+  a.w_bf16 = weights_dtype == MOE_DTYPE_BF16;
+  a.topk_idx = topk_index;
+  a.out_f32 = logits;
+  a.bias = expert_bias;
+  a.scaling = scaling_factor > 0.f ? scaling_factor : 0.f;
+  a.ngroups = num_groups > 0 ? num_groups : 0;
+  a.gtopk = num_groups > 0 ? group_topk : 0;
+  a.tpe = tokens_per_expert;
+  a.renorm = renormalize;
+  a.topk = K;
+  a.T = T; a.E = E; a.H = H; a.I = 64;
+  a.n_ct = (int)((T + BC - 1) / BC);
+  a.n_rt = 1;
+  MOE_REQUIRE(a.n_ct < (1 << 30), MOE_ERR_UNSUPPORTED, "%s: too many tiles", who);
+  a.n_tiles = a.n_ct;
+  if (E <= 64) return launch<RLTS, 64>(a, a.n_tiles, (hipStream_t)stream);
+  return launch<RLTS, 128>(a, a.n_tiles, (hipStream_t)stream);
 }
 
 namespace {

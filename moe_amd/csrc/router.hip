@@ -100,27 +100,6 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void softmax_topk_kernel(
   }
 }
 
-// The input of the DeepSeek router kernels: logits (scores = sigmoid,
-// fp32 arithmetic after it: src/models/router.py:107-138), or, with
-// scores_in, the scores themselves -- the reference's torch.sigmoid of bf16
-// logits under bf16 autocast, passed as fp32 values -- after which the
-// weights follow torch's bf16 arithmetic: their sum rounded to bf16 (+1e-20),
-// the quotient and the scaled weight each rounded to bf16.
-__device__ __forceinline__ float dsk_score(float x, int scores_in) {
-  return scores_in ? x : sigmoidf_(x);
-}
-__device__ __forceinline__ float dsk_weight(float v, float ssum, int renorm, float scaling,
-                                            int scores_in) {
-  if (scores_in) {
-    if (renorm) v = round_bf(v / round_bf(round_bf(ssum) + 1e-20f));
-    if (scaling > 0.f) v = round_bf(v * scaling);
-  } else {
-    if (renorm) v = v / (ssum + 1e-20f);
-    if (scaling > 0.f) v = v * scaling;
-  }
-  return v;
-}
-
 // DeepSeek router (flat top-k, no expert groups) with G lanes per token, as
 // softmax_topk_group_kernel: scores = sigmoid(logits) stored, selection by
 // rank keys of the biased scores, the winner's unbiased score taken from its

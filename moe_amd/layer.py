@@ -8,10 +8,10 @@ call the reference makes, so the logits and therefore the routing are the
 reference's, bit for bit) or the MFMA kernel (``gating="hip"``: the same
 exact bf16 products summed in the kernel's own fp32 order, so a top-k choice
 between experts whose logits tie within one bf16 rounding can differ); its
-backward runs on the MFMA kernels either way.  ``gating="hip_fused"`` (softmax
-router) runs the router in the MFMA gating kernel's epilogue: the same bits as
-"hip", without the logits' round trip (shapes the fused kernel does not cover
-take the two-kernel form, with the same results).
+backward runs on the MFMA kernels either way.  ``gating="hip_fused"`` runs the
+router (softmax, or DeepSeek sigmoid with E <= 128) in the MFMA gating kernel's
+epilogue: the same bits as "hip", without the logits' round trip (shapes the
+fused kernel does not cover take the two-kernel form, with the same results).
 ``SparseMoeBlock`` wraps it with the reference's parameter names
 (``gate.weight``, ``experts.gate_up_proj``, ``experts.down_proj``).
 """
@@ -22,7 +22,7 @@ from torch import nn
 
 from . import library  # registers the moe_amd:: ops
 from .experts import experts_forward
-from .router import gating_linear, sigmoid_topk, softmax_topk
+from .router import gating_linear, linear_sigmoid_topk, sigmoid_topk, softmax_topk
 
 
 def _fused_softmax_ok(x, w_router, gate_up_proj, down_proj) -> bool:
@@ -60,6 +60,10 @@ def moe_layer(x: torch.Tensor, w_router: torch.Tensor, gate_up_proj: torch.Tenso
     if router == "softmax":
         logits = gating_linear(x, w_router, fp32=False, hip=hip)
         probs, w, idx = softmax_topk(logits, top_k, renormalize, logit_offset)
+    elif router == "sigmoid" and gating == "hip_fused":
+        probs, w, idx = linear_sigmoid_topk(x, w_router, expert_bias, top_k, renormalize,
+                                            scaling_factor, num_groups, group_topk, x.dtype,
+                                            tokens_per_expert)
     elif router == "sigmoid":
         logits = gating_linear(x, w_router, fp32=True, hip=hip)
         probs, w, idx = sigmoid_topk(logits, expert_bias, top_k, renormalize, scaling_factor,

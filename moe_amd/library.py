@@ -15,6 +15,9 @@ differentiable piece of the MI355X path, each a functional op in namespace
   router_linear / _backward      the gating linear on the MFMA kernel
   softmax_topk / _backward       Qwen3MoeTopKRouter's softmax + top-k
   sigmoid_topk / _backward       DeepSeekRouter's sigmoid + biased top-k
+  linear_sigmoid_topk            its fp32 gating linear and the router in one
+                                 kernel (backward: sigmoid_topk_backward, then
+                                 router_linear_backward)
 
 A forward op returns, besides its results, the tensors its backward needs
 (the routing plan, gate_up), so that setup_context saves only op outputs; the
@@ -440,6 +443,65 @@ def _sigmoid_backward(ctx, d_scores, d_w, d_idx, d_counts):
 
 torch.library.register_autograd(f"{_LIB}::sigmoid_topk", _sigmoid_backward,
                                 setup_context=_sigmoid_setup)
+
+
+@torch.library.custom_op(f"{_LIB}::linear_sigmoid_topk", mutates_args=())
+def linear_sigmoid_topk(x: Tensor, w_router: Tensor, expert_bias: Optional[Tensor], top_k: int,
+                        renormalize: bool, scaling_factor: float, num_groups: int,
+                        group_topk: int, weights_dtype: torch.dtype, count: bool
+                        ) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """The DeepSeek router with its fp32 gating linear in one kernel: (scores
+    fp32 [T,E], weights [T,K], index [T,K], selection counts fp32 [E] (zeros
+    unless count)); the same bits as router_linear(fp32) + sigmoid_topk
+    (src/models/router.py:103-152)."""
+    counts = torch.zeros(w_router.shape[0], device=x.device, dtype=torch.float32)
+    scores, w, idx = ops.router_linear_sigmoid_topk(
+        x, w_router, expert_bias, top_k, renormalize, scaling_factor or None,
+        num_groups or None, group_topk or None, weights_dtype, counts if count else None)
+    return scores, w, idx, counts
+
+
+@linear_sigmoid_topk.register_fake
+def _(x, w_router, expert_bias, top_k, renormalize, scaling_factor, num_groups, group_topk,
+      weights_dtype, count):
+    T, E = x.shape[0], w_router.shape[0]
+    dev = x.device
+    return (torch.empty(T, E, device=dev, dtype=torch.float32),
+            torch.empty(T, top_k, device=dev, dtype=weights_dtype),
+            torch.empty(T, top_k, device=dev, dtype=torch.int64),
+            torch.empty(E, device=dev, dtype=torch.float32))
+
+
+def _linear_sigmoid_setup(ctx, inputs, output):
+    x, w_router, _, _, renormalize, scaling_factor, _, _, weights_dtype, _ = inputs
+    scores, _, idx, counts = output
+    ctx.set_materialize_grads(False)
+    ctx.mark_non_differentiable(idx, counts)
+    ctx.save_for_backward(x, w_router, scores, idx)
+    ctx.renormalize = renormalize
+    ctx.scaling_factor = scaling_factor
+    ctx.w_dtype = weights_dtype
+
+
+def _linear_sigmoid_backward(ctx, d_scores, d_w, d_idx, d_counts):
+    """The router's backward (sigmoid_topk_backward: gather, renormalisation,
+    scaling, sigmoid) into the fp32 gating linear's two gradients."""
+    x, w_router, scores, idx = ctx.saved_tensors
+    need_x, need_wr = (bool(n) for n in ctx.needs_input_grad[:2])
+    none = (None,) * 8
+    if (d_scores is None and d_w is None) or not (need_x or need_wr):
+        return (None, None) + none
+    if d_w is None:
+        d_w = torch.zeros(idx.shape, device=idx.device, dtype=ctx.w_dtype)
+    d_logits = torch.ops.moe_amd.sigmoid_topk_backward(scores, idx, d_w.to(ctx.w_dtype), d_scores,
+                                                       ctx.renormalize, ctx.scaling_factor)
+    dx, dw = torch.ops.moe_amd.router_linear_backward(d_logits, x, w_router, torch.float32,
+                                                      need_x, need_wr)
+    return (dx if need_x else None, dw if need_wr else None) + none
+
+
+torch.library.register_autograd(f"{_LIB}::linear_sigmoid_topk", _linear_sigmoid_backward,
+                                setup_context=_linear_sigmoid_setup)
 
 
 # ------------------------------------------------ softmax layer, one node

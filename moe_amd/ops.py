@@ -181,6 +181,51 @@ def router_linear_softmax_topk(x: torch.Tensor, weight: torch.Tensor, top_k: int
     return (probs, w, idx, logits) if return_logits else (probs, w, idx)
 
 
+def router_fused_sigmoid_supported(E: int, top_k: int, num_groups: int | None = None) -> bool:
+    """Shapes of router_linear_sigmoid_topk: 8 lanes per token, 8 or 16
+    experts per lane, each expert group scored on one lane."""
+    return E % 8 == 0 and E <= 128 and top_k <= 8 and (not num_groups or num_groups <= 8)
+
+
+@on_tensor_device
+def router_linear_sigmoid_topk(x: torch.Tensor, weight: torch.Tensor,
+                               expert_bias: torch.Tensor | None, top_k: int,
+                               renormalize: bool = True, scaling_factor: float | None = None,
+                               num_groups: int | None = None, group_topk: int | None = None,
+                               weights_dtype: torch.dtype = torch.float32,
+                               tokens_per_expert: torch.Tensor | None = None,
+                               return_logits: bool = False):
+    """The gating linear with the DeepSeek-V3 router fused into its epilogue:
+    (scores fp32 [T,E], weights [T,K] in weights_dtype, index int64 [T,K][,
+    fp32 logits [T,E]]), bit-identical to router_linear(x, weight, fp32)
+    followed by router_sigmoid_topk with the same arguments; with
+    ``tokens_per_expert`` the selection counts are added to it."""
+    _need_cuda(x, weight, expert_bias, tokens_per_expert)
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise TypeError("router_linear_sigmoid_topk takes bf16 hidden states and weight")
+    x = _contig(x)
+    weight = _contig(weight)
+    T, H = x.shape
+    E = weight.shape[0]
+    if weight.shape[1] != H:
+        raise ValueError(f"router_linear_sigmoid_topk: weight {tuple(weight.shape)} vs hidden "
+                         f"{tuple(x.shape)}")
+    dev = x.device
+    scores = torch.empty(T, E, device=dev, dtype=torch.float32)
+    w = torch.empty(T, top_k, device=dev, dtype=weights_dtype)
+    idx = torch.empty(T, top_k, device=dev, dtype=torch.int64)
+    logits = torch.empty(T, E, device=dev, dtype=torch.float32) if return_logits else None
+    if expert_bias is not None:
+        expert_bias = _contig(expert_bias.to(torch.float32))
+    grouped = num_groups is not None and group_topk is not None
+    _call("moe_amd_router_linear_sigmoid_topk", x.data_ptr(), weight.data_ptr(), T, E, H,
+          _ptr(expert_bias), int(top_k), int(renormalize), float(scaling_factor or 0.0),
+          int(num_groups) if grouped else 0, int(group_topk) if grouped else 0,
+          scores.data_ptr(), w.data_ptr(), _dtype_code(weights_dtype), idx.data_ptr(),
+          _ptr(tokens_per_expert), _ptr(logits), _stream(x))
+    return (scores, w, idx, logits) if return_logits else (scores, w, idx)
+
+
 @on_tensor_device
 def router_linear_backward_dx(d_logits: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     """d_x [T,H] = bf16(d_logits [T,E] . weight [E,H]) on MFMA (bf16 inputs)."""

@@ -79,6 +79,35 @@ def sigmoid_topk(logits: torch.Tensor, expert_bias: torch.Tensor | None, top_k: 
     return scores, w, idx
 
 
+def linear_sigmoid_topk(x: torch.Tensor, weight: torch.Tensor, expert_bias: torch.Tensor | None,
+                        top_k: int, renormalize: bool = True,
+                        scaling_factor: float | None = None, num_groups: int | None = None,
+                        group_topk: int | None = None,
+                        weights_dtype: torch.dtype = torch.float32,
+                        tokens_per_expert: torch.Tensor | None = None):
+    """(hidden states) -> (scores, weights, index) of the DeepSeek-V3 router
+    with its fp32 gating linear fused into one MFMA kernel (op
+    ``moe_amd::linear_sigmoid_topk``); the results of ``gating_linear`` with
+    ``hip=True`` followed by ``sigmoid_topk``, bit for bit.  Shapes outside
+    the fused kernel's (``ops.router_fused_sigmoid_supported``) take those
+    two steps."""
+    grouped = num_groups is not None and group_topk is not None
+    E = weight.shape[0]
+    if not (x.is_cuda and x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16
+            and x.shape[1] % 64 == 0
+            and ops.router_fused_sigmoid_supported(E, top_k, num_groups if grouped else None)):
+        logits = gating_linear(x, weight, fp32=True, hip=True)
+        return sigmoid_topk(logits, expert_bias, top_k, renormalize, scaling_factor, num_groups,
+                            group_topk, weights_dtype, tokens_per_expert)
+    scores, w, idx, counts = torch.ops.moe_amd.linear_sigmoid_topk(
+        x, weight, expert_bias, int(top_k), bool(renormalize), float(scaling_factor or 0.0),
+        int(num_groups) if grouped else 0, int(group_topk) if grouped else 0, weights_dtype,
+        tokens_per_expert is not None)
+    if tokens_per_expert is not None:
+        tokens_per_expert.add_(counts)
+    return scores, w, idx
+
+
 class MI355XTopKRouter(_RouterBase):
     """Softmax top-k router (Qwen3MoeTopKRouter.forward,
     src/models/modeling_qwen3_moe.py:266-275): returns
@@ -127,15 +156,23 @@ class MI355XDeepSeekRouter(_RouterBase):
         self._last_top_k_idx = None
 
     hip_gating_linear = False  # True: MFMA gating linear with fp32 logits
+    fused_router = False       # True: that gating linear with the router in its epilogue
 
     def forward(self, hidden_states):
         hidden_states = hidden_states.reshape(-1, self.hidden_dim)
-        logits = gating_linear(hidden_states, self.weight, fp32=True, hip=self.hip_gating_linear)
         counting = torch.is_grad_enabled()
+        tpe = self.local_tokens_per_expert if counting else None
+        if self.fused_router:
+            scores, w, idx = linear_sigmoid_topk(
+                hidden_states, self.weight, self.expert_bias, self.top_k,
+                bool(self.norm_topk_prob), self.scaling_factor, self.num_groups, self.group_topk,
+                hidden_states.dtype, tpe)
+            self._last_top_k_idx = idx.detach()
+            return scores, w, idx
+        logits = gating_linear(hidden_states, self.weight, fp32=True, hip=self.hip_gating_linear)
         scores, w, idx = sigmoid_topk(
             logits, self.expert_bias, self.top_k, bool(self.norm_topk_prob), self.scaling_factor,
-            self.num_groups, self.group_topk, hidden_states.dtype,
-            self.local_tokens_per_expert if counting else None)
+            self.num_groups, self.group_topk, hidden_states.dtype, tpe)
         self._last_top_k_idx = idx.detach()
         return scores, w, idx
 
