@@ -277,14 +277,14 @@ int moe_amd_gemm_down_backward_dw(const void* dy, const void* act, const int32_t
 
 /* The combine's backward fused into GEMM-2's backward, without the [S,H]
  * d_y = w * d_out[token] of moe_amd_combine_backward: per routed row r of
- * token t = row_src[r]/K, g = d_out[t] @ down_proj[e] (bf16-rounded);
+ * token t = row_src[r]/K, g = d_out[t] @ down_proj[e] (fp32 sums);
  * d_act = w[row_src[r]] * g and (d_gate, d_up) from gate_up as in
  * moe_amd_gemm_down_backward_dx_dswiglu -> d_gate_up [S,2I];
  * act_w [S,I] = w * act (act = silu(gate) * up recomputed from gate_up,
  * bitwise as the forward stored it), the input of
  * moe_amd_gemm_down_backward_dw_gathered; dw_partials
- * [T*K][moe_amd_gemm_down_backward_dx_fused_parts(I)] fp32: per column
- * tile, <g, act> over its columns = that tile's share of
+ * [T*K][moe_amd_gemm_down_backward_dx_fused_parts(I)] fp32: per 128
+ * features, <g, act> over them = that block's share of
  * d_w[t,k] = <d_out[t], y[r]>, reduced by moe_amd_weight_grad_reduce.
  * topk_weights [T*K] in weights_dtype (fp32 or bf16).  Replaces the
  * autograd of transformers/integrations/moe.py:457-478 (weights multiply,

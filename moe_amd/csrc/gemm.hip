@@ -195,26 +195,6 @@ __device__ __forceinline__ int div_topk(int n, uint32_t m, int shift) {
   return (int)(((uint64_t)(uint32_t)n * m) >> shift);
 }
 
-// Sum over each 32-lane half of the wave, returned in every lane of that
-// half, in a fixed order: DPP within rows of 16 (quad xor 1, quad xor 2,
-// half-row mirror, row mirror), then the two rows' totals by v_readlane.
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
-}
-__device__ __forceinline__ float half_wave_sum(float v) {
-  v += dpp_f<0xB1>(v);
-  v += dpp_f<0x4E>(v);
-  v += dpp_f<0x141>(v);
-  v += dpp_f<0x140>(v);
-  const int iv = __float_as_int(v);
-  const float s0 = __int_as_float(__builtin_amdgcn_readlane(iv, 0)) +
-                   __int_as_float(__builtin_amdgcn_readlane(iv, 16));
-  const float s1 = __int_as_float(__builtin_amdgcn_readlane(iv, 32)) +
-                   __int_as_float(__builtin_amdgcn_readlane(iv, 48));
-  return (threadIdx.x & 32) ? s1 : s0;
-}
-
 // Logistic sigmoid from the hardware base-2 exponential and reciprocal
 // (v_exp_f32, v_rcp_f32; about 1 ulp each): 1 / (1 + 2^(-x log2 e)).  The
 // epilogues evaluate it once per output element, where an IEEE expf and
@@ -264,7 +244,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
   // PF: the next tile's first stages are issued before this tile's epilogue,
   // which is wave-local and issues exactly NST stores per wave.
   constexpr bool PF = MODE == G1F || MODE == G2F || MODE == G1DX || MODE == G1DW || MODE == G2DWG ||
-                      MODE == RDX;
+                      MODE == RDX || MODE == G2DXF;
   constexpr int NST = (MODE == G1F ? 12 : 8) * TJ;
   static_assert(!PF || FPW + NST <= 63, "vmcnt range");
   static_assert(TOKEN || DENSE || BR == 256, "dW modes use 256-row tiles");
@@ -416,8 +396,13 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       return (uint32_t)st;
     }
   };
-  int erow_src = 0;        // G2DXF: row_src of tile row tid
-  uint32_t erow_wraw = 0;  // ... and its routing weight's bits (fp32, or bf16 zero-extended)
+  // G2DXF: row_src of this lane's tile rows (wr*WR + j*32 + l32, j < TJ) of
+  // the tile that setup() prepared (nsrc) and of the tile being computed
+  // (csrc), and the latter's routing weights (raw bits: fp32, or bf16
+  // zero-extended).  The epilogue of one tile runs after the next tile's
+  // setup, so each tile's values pass from the n- to the c-set at the hand-over.
+  int nsrc[TOKEN ? TJ : 1], csrc[TOKEN ? TJ : 1];
+  uint32_t cwr[TOKEN ? TJ : 1];
 
   auto setup = [&](const Tile& d) {
     kb_cur = d.kbeg;
@@ -537,8 +522,11 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
     if constexpr (GCOL) isrc = make_rsrc(p.row_src, (uint32_t)(p.S * 4));
     // G2DXF: row_src of tile row tid, consumed by the epilogue (the load
     // completes under the main loop).
-    if constexpr (MODE == G2DXF)
-      if (tid < BR) erow_src = p.row_src[min(d.row0 + tid, d.row_end - 1)];
+    if constexpr (MODE == G2DXF) {
+#pragma unroll
+      for (int j = 0; j < TJ; ++j)
+        nsrc[j] = p.row_src[min(d.row0 + wr * WR + j * 32 + l32, d.row_end - 1)];
+    }
   };
 
   // G1DW, G2DWG: raw row_src entries of stage s, one 64-lane load per wave
@@ -681,15 +669,6 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       tok_offsets(1, tk_b);
       if constexpr (ROW_FIRST) issue_row(1);
       else issue_col(1, tk_b);
-      if constexpr (MODE == G2DXF) {
-        // The row's routing weight, in flight under the main loop (raw bits:
-        // converting here would wait for the load).  Being the youngest op,
-        // it makes the first stage wait cover one more column block, which
-        // only strengthens it.
-        if (tid < BR)
-          erow_wraw = p.rw_bf16 ? (uint32_t)((const uint16_t*)p.rw)[erow_src]
-                                : ((const uint32_t*)p.rw)[erow_src];
-      }
   };
   // Main loop of tile `cur` (its prologue issued).  after_epi: the previous
   // tile's epilogue stores were issued after this tile's prologue (PF modes).
@@ -757,7 +736,10 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       if constexpr (PF) {
         // the previous tile's NST epilogue stores were issued after this
         // tile's first stages: they may still be in flight
-        if (after_epi) WAIT_VMCNT_LGKM0(FPW + NST);
+        // (G2DXF: its epilogue waited for gate/up loads issued after this
+        // tile's first stages, and loads complete in issue order, so those
+        // stages have landed; only its trailing stores may be in flight.)
+        if (after_epi) WAIT_VMCNT_LGKM0(MODE == G2DXF ? 63 : FPW + NST);
         else WAIT_VMCNT_LGKM0(FPW);
       } else {
         WAIT_VMCNT_LGKM0(FPW);
@@ -895,7 +877,134 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
           }
       }
     };
-    if constexpr (MODE == G1F) {
+    if constexpr (MODE == G2DXF) {
+      // g = d_out[token] . down_proj[e] (fp32) leaves through this wave's
+      // 16 KB region one row sub-tile (32 rows x 128 features) at a time,
+      // 512-byte rows with 16-byte chunks XOR-swizzled by row, and is read
+      // back in row order: 16 lanes per row, 8 features per lane, so every
+      // gate/up load and every store moves 256 contiguous bytes per row.
+      // Per element: d_act = w * g; act = bf16(bf16(silu(gate)) * up)
+      // recomputed exactly as G1F stored it; d_up = bf16(d_act * silu),
+      // d_gate = bf16(bf16(d_act * up) * sigmoid'); w * act for the dW
+      // GEMM; and the weight-gradient partial sum of g * act over the
+      // wave's 128 features (a lane's 8 in order, then a fixed butterfly
+      // over the row's 16 lanes), stored per (row, column tile, wave
+      // column).  Rows and features outside the output get offsets past
+      // the descriptors' extents: loads return 0, stores are dropped.
+      constexpr int NIT = 8;  // iterations of 4 rows per row sub-tile
+      const int fw = c.ct * BC + ewc * 128;
+      const int nr = c.row_end - c.row0;  // >= 1
+      const int c8 = (ln & 15) * 8, rq = ln >> 4;
+      const bool fok = fw + c8 < I;
+      const auto rgu = make_rsrc(p.a1 + (int64_t)c.row0 * I2, (uint32_t)nr * (uint32_t)I2 * 2);
+      const auto rdg = make_rsrc(p.out + (int64_t)c.row0 * I2, (uint32_t)nr * (uint32_t)I2 * 2);
+      const auto raw = make_rsrc(p.out2 + (int64_t)c.row0 * I, (uint32_t)nr * (uint32_t)I * 2);
+      const int n_part = 2 * p.n_ct;
+      // Byte offsets of the lane's first row and features; row j*32 + it*4
+      // further adds a wave-uniform step.  lim: the lane's rows are valid
+      // while that step's row count stays below it (never, for features
+      // past I).
+      const int r0l = ewr * WR + rq;
+      const int lim = fok ? nr - r0l : INT32_MIN;
+      const uint32_t bg = (uint32_t)r0l * (uint32_t)(I2 * 2) + (uint32_t)(fw + c8) * 2;
+      const uint32_t ba = (uint32_t)r0l * (uint32_t)(I * 2) + (uint32_t)(fw + c8) * 2;
+      auto og = [&](int j, int it) -> uint32_t {  // gate bytes of (row, lane's features)
+        const int d = j * 32 + it * 4;
+        return d < lim ? bg + (uint32_t)d * (uint32_t)(I2 * 2) : kOOB;
+      };
+      auto oa = [&](int j, int it) -> uint32_t {
+        const int d = j * 32 + it * 4;
+        return d < lim ? ba + (uint32_t)d * (uint32_t)(I * 2) : kOOB;
+      };
+      // gate/up of iteration n = j*NIT + it are loaded PD iterations ahead
+      // (HBM latency: one iteration's arithmetic is ~1 k cycles)
+      constexpr int PD = 8, NN = TJ * NIT;
+      u32x4 gl[PD], ul[PD];
+      auto load = [&](int n) {
+        const uint32_t o = og(n / NIT, n % NIT);
+        gl[n % PD] = __builtin_amdgcn_raw_buffer_load_b128(rgu, o, 0, 2);
+        ul[n % PD] = __builtin_amdgcn_raw_buffer_load_b128(rgu, o + (uint32_t)I * 2, 0, 2);  // kOOB stays out
+      };
+#pragma unroll
+      for (int n = 0; n < PD && n < NN; ++n) load(n);
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) {
+        // accumulator rows of sub-tile j -> region, fp32
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int ch = 8 * i + 2 * q + ehl;
+            *(__attribute__((address_space(3))) f32x4*)(reg + el32 * 512 + ((ch ^ el32) << 4)) =
+                f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                      acc[i][j][4 * q + 3]};
+          }
+        // the routing weights and row_src of the lane's eight rows of this
+        // sub-tile, from the lanes that hold them (fetched together)
+        uint32_t wq[NIT];
+        int sq[NIT];
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+          wq[it] = (uint32_t)__shfl((int)cwr[j], it * 4 + rq, 64);
+          sq[it] = __shfl(csrc[j], it * 4 + rq, 64);
+        }
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+          const int n = j * NIT + it, b = n % PD;
+          const int r = it * 4 + rq;  // row within the sub-tile
+          const int lc = c8 >> 2;     // logical chunk of the lane's first 4 features
+          const f32x4 g0 = *(const __attribute__((address_space(3))) f32x4*)(
+              reg + r * 512 + ((lc ^ r) << 4));
+          const f32x4 g1 = *(const __attribute__((address_space(3))) f32x4*)(
+              reg + r * 512 + (((lc + 1) ^ r) << 4));
+          const float wgt = __uint_as_float(p.rw_bf16 ? wq[it] << 16 : wq[it]);
+          float gq[8], g[8], u[8], sg[8], t[8], sl[8], a[8], da[8], ds[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            gq[e] = e < 4 ? g0[e] : g1[e - 4];
+            g[e] = (e & 1) ? bf_hi(gl[b][e >> 1]) : bf_lo(gl[b][e >> 1]);
+            u[e] = (e & 1) ? bf_hi(ul[b][e >> 1]) : bf_lo(ul[b][e >> 1]);
+            sg[e] = fast_sigmoid(g[e]);
+            t[e] = g[e] * sg[e];
+          }
+          // bf16 roundings two at a time (one v_cvt_pk_bf16_f32 per pair)
+          u32x4 dgv, duv, awv;
+          float dot = 0.f;
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const int e0 = 2 * w, e1 = 2 * w + 1;
+            const uint32_t slp = pack_bf2(t[e0], t[e1]);
+            sl[e0] = bf_lo(slp);
+            sl[e1] = bf_hi(slp);
+            const uint32_t ap = pack_bf2(sl[e0] * u[e0], sl[e1] * u[e1]);
+            a[e0] = bf_lo(ap);
+            a[e1] = bf_hi(ap);
+            da[e0] = wgt * gq[e0];
+            da[e1] = wgt * gq[e1];
+            const uint32_t dsp = pack_bf2(da[e0] * u[e0], da[e1] * u[e1]);
+            ds[e0] = bf_lo(dsp);
+            ds[e1] = bf_hi(dsp);
+            // sigmoid'(g) (1 + g) form: sg (1 + g (1 - sg)) = sg + t (1 - sg)
+            dgv[w] = pack_bf2(ds[e0] * fmaf(t[e0], 1.f - sg[e0], sg[e0]),
+                              ds[e1] * fmaf(t[e1], 1.f - sg[e1], sg[e1]));
+            duv[w] = pack_bf2(da[e0] * sl[e0], da[e1] * sl[e1]);
+            awv[w] = pack_bf2(wgt * a[e0], wgt * a[e1]);
+            dot = fmaf(gq[e0], a[e0], dot);
+            dot = fmaf(gq[e1], a[e1], dot);
+          }
+          if (n + PD < NN) load(n + PD);
+          const uint32_t o = og(j, it), oaw = oa(j, it);
+          __builtin_amdgcn_raw_buffer_store_b128(dgv, rdg, o, 0, 2);
+          __builtin_amdgcn_raw_buffer_store_b128(duv, rdg, o + (uint32_t)I * 2, 0, 2);
+          __builtin_amdgcn_raw_buffer_store_b128(awv, raw, oaw, 0, 2);
+          // the row's partial over the wave's 128 features
+          const float tot = group_sum<16>(fok ? dot : 0.f);
+          if ((ln & 15) == 0 && j * 32 + it * 4 < nr - r0l)
+            p.dw_part[(int64_t)sq[it] * n_part + c.ct * 2 + ewc] = tot;
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    } else if constexpr (MODE == G1F) {
       // tile columns of this wave: [gate 64 | up 64] of features fb..fb+63
       const int fb = c.ct * 128 + ewc * 64;
       const int r0 = c.row0 + ewr * WR;
@@ -990,11 +1099,25 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
 #pragma unroll
   for (int j = 0; j < SV; ++j) scnt[j] = 0;
   if constexpr (PF) {
+    // G2DXF: the rows prepared by the last setup() become the computed
+    // tile's, and their routing weights are fetched (in flight under the
+    // main loop; first used by the epilogue).
+    auto take_rows = [&]() {
+      if constexpr (MODE == G2DXF) {
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+          csrc[j] = nsrc[j];
+          cwr[j] = p.rw_bf16 ? (uint32_t)((const uint16_t*)p.rw)[nsrc[j]]
+                             : ((const uint32_t*)p.rw)[nsrc[j]];
+        }
+      }
+    };
     // (a dynamic walk may find no tile at all; every workgroup still
     // reaches the finished-count update below)
     Tile cur = decode(dyn ? max(t, 0) : t);
     if (dyn ? t >= 0 : t < t_end) setup(cur);
     if ((dyn ? t >= 0 : t < t_end) && cur.nk > 0) prologue();
+    if (dyn ? t >= 0 : t < t_end) take_rows();
     bool first = true;
     while (dyn ? t >= 0 : t < t_end) {
 #pragma unroll
@@ -1019,6 +1142,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       }
       epilogue_pf(cur);
       if (!more) break;
+      take_rows();
       cur = nxt;
       t = tn_next;
       first = false;
@@ -1204,15 +1328,6 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
             *(u32x2*)(stg + row * SROW + col) = v;
           }
         }
-    // G2DXF: each tile row's routing weight and row_src, past the staging tile.
-    float* const erow_w = (float*)(stg + BR * SROW);
-    int* const erow_s = (int*)(erow_w + BR);
-    if constexpr (MODE == G2DXF) {
-      if (tid < BR) {
-        erow_w[tid] = __uint_as_float(p.rw_bf16 ? erow_wraw << 16 : erow_wraw);
-        erow_s[tid] = erow_src;
-      }
-    }
     __syncthreads();
     if constexpr (MODE == G1F) {
       // 128 output features per tile; 16 lanes x 8 features per row, in
@@ -1254,18 +1369,14 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
         }
       }
     } else if constexpr (DOWN_DX) {
-      // d_act tile (bf16) -> d_gate, d_up with gate/up read back from gate_up.
-      // G2DXF: the tile holds g = d_out[token] . down_proj[e] instead, and
-      // per row d_act = w * g, the weight gradient's partial g . act over
-      // the tile's columns (act = silu(gate) * up recomputed exactly as the
-      // forward stored it), and w * act for the dW GEMM.
+      // G2DX (the unfused form; G2DXF has its own epilogue): d_act tile
+      // (bf16) -> d_gate, d_up with gate/up read back from gate_up.
       // Each thread owns NB batches of RB rows; the gate/up loads of batch
       // b+1 are issued before batch b is computed and stored, so loads never
       // queue behind this thread's stores.  Loads are clamped in bounds
       // (rows past the tile's end re-read its last row) and only the stores
       // are predicated.
-      constexpr bool FUSED = MODE == G2DXF;
-      constexpr int RB = FUSED ? 4 : 8, NB = BR / (RB * (NTHR / 32));  // FUSED: ~256 VGPRs
+      constexpr int RB = 8, NB = BR / (RB * (NTHR / 32));
       const int c0 = (tid & 31) * 8;
       const int f = cur.ct * BC + c0;
       const bool fok = f < I;
@@ -1289,43 +1400,27 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
           const int row = (tid >> 5) + (b * RB + q) * (NTHR / 32);
           const int r = cur.row0 + row;
           const u32x4 dav = *(const u32x4*)(stg + row * SROW + c0);
-          const float wgt = FUSED ? erow_w[row] : 1.f;
-          float dot = 0.f;
-          u32x4 dgv, duv, awv;
+          u32x4 dgv, duv;
 #pragma unroll
           for (int w = 0; w < 4; ++w) {
-            float dg[2], du[2], aw[2];
+            float dg[2], du[2];
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-              const float gq = h ? bf_hi(dav[w]) : bf_lo(dav[w]);
+              const float da = h ? bf_hi(dav[w]) : bf_lo(dav[w]);
               const float g = h ? bf_hi(gv[b & 1][q][w]) : bf_lo(gv[b & 1][q][w]);
               const float u = h ? bf_hi(uv[b & 1][q][w]) : bf_lo(uv[b & 1][q][w]);
               const float sg = fast_sigmoid(g);
               const float sl = round_bf(g * sg);          // silu(g) as stored in bf16
-              const float da = FUSED ? wgt * gq : gq;
               const float ds = round_bf(da * u);          // d silu(g)
               du[h] = da * sl;
               dg[h] = ds * (sg * (1.f + g * (1.f - sg)));
-              if constexpr (FUSED) {
-                const float a = round_bf(sl * u);         // act as the forward stored it
-                dot += gq * a;
-                aw[h] = wgt * a;
-              }
             }
             dgv[w] = pack_bf2(dg[0], dg[1]);
             duv[w] = pack_bf2(du[0], du[1]);
-            if constexpr (FUSED) awv[w] = pack_bf2(aw[0], aw[1]);
-          }
-          if constexpr (FUSED) {
-            // Sum over the row's 32 lanes in a fixed order (deterministic).
-            const float tot = half_wave_sum(fok ? dot : 0.f);
-            if ((lane & 31) == 0 && r < cur.row_end)
-              p.dw_part[(int64_t)erow_s[row] * p.n_ct + cur.ct] = tot;
           }
           if (r < cur.row_end && fok) {
             __builtin_nontemporal_store(dgv, (u32x4*)(p.out + (int64_t)r * I2 + f));
             __builtin_nontemporal_store(duv, (u32x4*)(p.out + (int64_t)r * I2 + I + f));
-            if constexpr (FUSED) __builtin_nontemporal_store(awv, (u32x4*)(p.out2 + (int64_t)r * I + f));
           }
         }
       }
@@ -1503,13 +1598,11 @@ int num_cus() {
 template <int MODE, int BR>
 int launch(const GemmArgs& a, int max_tiles, hipStream_t st) {
   constexpr size_t stages = (size_t)NSLOT * SLOT;
-  // staging tile ([BC][SROW] when transposed), plus G2DXF's per-row weights
-  // and row_src
+  // staging tile of the non-PF epilogues ([BC][SROW] when transposed)
   constexpr size_t staging =
       MODE == RLTS ? (size_t)BC * (BR + 4) * sizeof(float)  // fp32 logits [token][expert]
                    : (size_t)((MODE == G2DWG || MODE == RLT || MODE == RLTK) ? BC : BR) * SROW *
-                             sizeof(bf16) +
-                         (MODE == G2DXF ? (size_t)BR * 8 : 0);
+                         sizeof(bf16);
   const size_t lds = stages > staging ? stages : staging;
   if (max_tiles <= 0) return MOE_OK;
   hipError_t err = hipFuncSetAttribute((const void*)grouped_gemm_kernel<MODE, BR>,
@@ -2049,7 +2142,9 @@ extern "C" int moe_amd_gemm_down_backward_dx_dswiglu(const void* dy, const int32
   return launch_token<G2DX>(a, S, E, BC, I, tile_plan, (hipStream_t)stream);
 }
 
-extern "C" int moe_amd_gemm_down_backward_dx_fused_parts(int I) { return (I + BC - 1) / BC; }
+// Two weight-gradient partials per routed row and 256-feature column tile
+// (one per wave column of 128 features).
+extern "C" int moe_amd_gemm_down_backward_dx_fused_parts(int I) { return 2 * ((I + BC - 1) / BC); }
 
 extern "C" int moe_amd_gemm_down_backward_dx_fused(
     const void* d_out, const int32_t* row_src, int top_k, const int32_t* offsets,
