@@ -364,6 +364,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
   const char* cptr = nullptr;
   const char* rptr = nullptr;
   uint32_t cbytes = 0, rbytes = 0;
+  uint64_t rbytes64 = 0;  // dW modes: the expert's k-major row operand, any size
   __amdgpu_buffer_rsrc_t isrc;
   uint32_t coff[CPW];  // byte offsets of this lane's column blocks at stage 0
   uint32_t roff[RPW];
@@ -394,6 +395,22 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       return (uint32_t)v;
     } else {
       return (uint32_t)st;
+    }
+  };
+  // The dW modes' row operand (one expert's rows, k-major) is rebased per
+  // stage in 64 bits: an expert may own more than 4 GB of rows (a token
+  // listing one expert several times is accepted), and a stage reads at
+  // most rstep bytes past its base, so the extent is capped, not wrapped.
+  auto row_stage_rsrc = [&](int s) {
+    if constexpr (ROW_KM) {
+      const uint64_t adv = (uint64_t)(uint32_t)s * rstep;
+      const uint64_t left = (s < nk_cur && adv < rbytes64) ? rbytes64 - adv : 0ull;
+      return make_rsrc(rptr + adv, __builtin_amdgcn_readfirstlane(
+                                       (uint32_t)(left < 0xfffff000ull ? left : 0xfffff000ull)));
+    } else {
+      const uint32_t adv = kst(s) * rstep;
+      return make_rsrc(rptr + adv, __builtin_amdgcn_readfirstlane(
+                                       (s < nk_cur && adv < rbytes) ? rbytes - adv : 0u));
     }
   };
   // G2DXF: row_src of this lane's tile rows (wr*WR + j*32 + l32, j < TJ) of
@@ -511,7 +528,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
     } else {
       const int ld = (MODE == G2DW) ? H : (MODE == RDW ? p.E : (MODE == G2DWG ? I : I2));
       rptr = (const char*)(p.a0 + (int64_t)d.kbeg * ld);
-      rbytes = (uint32_t)((int64_t)(d.kend - d.kbeg) * ld * 2);
+      rbytes64 = (uint64_t)(d.kend - d.kbeg) * (uint64_t)ld * 2;
 #pragma unroll
       for (int i = 0; i < RPW; ++i) {
         const int k = km_krow(wid + NW * i);
@@ -574,7 +591,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
   // DMA of the row half of stage s (ring position 2s+1, or 2s if ROW_FIRST).
   auto issue_row = [&](int s) {
     char* base = slot_ptr(2 * s + (ROW_FIRST ? 0 : 1));
-    const auto rs = stage_rsrc(rptr, rbytes, kst(s) * rstep, s);
+    const auto rs = row_stage_rsrc(s);
 #pragma unroll
     for (int i = 0; i < RPW; ++i) dma16(rs, roff[i], base + (wid + NW * i) * 1024);
   };
@@ -684,7 +701,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       // begins in the last sub-step of the stage before, so its second-half
       // descriptor is formed once there and carried into the next iteration.
       static_assert(TI * NOPS / NGRP <= NTOK + SPW, "a window's first TI groups hold no first-half op");
-      auto row_rsrc = [&](int s) { return stage_rsrc(rptr, rbytes, kst(s) * rstep, s); };
+      auto row_rsrc = [&](int s) { return row_stage_rsrc(s); };
       auto col_rsrc = [&](int s) { return stage_rsrc(cptr, cbytes, kst(s) * cstep, s); };
       // descriptors of the second half of stage s and the first half of stage s
       auto second_rsrc = [&](int s) { return ROW_FIRST ? col_rsrc(s) : row_rsrc(s); };
@@ -2265,10 +2282,6 @@ extern "C" int moe_amd_gemm_down_backward_dw_gathered(const void* d_out, const v
   MOE_REQUIRE(top_k >= 1 && S == T * top_k, MOE_ERR_ARG, "%s: S != T*top_k", who);
   MOE_REQUIRE(T * (int64_t)H * 2 < ((int64_t)1 << 31), MOE_ERR_UNSUPPORTED, "%s: T*H too large",
               who);
-  // One expert's act_w rows -- at most T, a token's K expert ids being
-  // distinct -- are addressed with 32-bit offsets.
-  MOE_REQUIRE(T * (int64_t)I * 2 < ((int64_t)1 << 32), MOE_ERR_UNSUPPORTED, "%s: T*I too large",
-              who);
   MOE_REQUIRE((S == 0 || (d_out && act_w && row_src)) && offsets && d_down_proj, MOE_ERR_ARG,
               "%s: null pointer", who);
   if (S > 0) {
@@ -2304,10 +2317,6 @@ extern "C" int moe_amd_gemm_gate_up_backward_dw(const void* d_gate_up, const voi
   if (rc) return rc;
   MOE_REQUIRE(top_k >= 1 && S == T * top_k, MOE_ERR_ARG, "%s: S != T*top_k", who);
   MOE_REQUIRE(T * (int64_t)H * 2 < ((int64_t)1 << 31), MOE_ERR_UNSUPPORTED, "%s: T*H too large",
-              who);
-  // One expert's d_gate_up rows -- at most T, a token's K expert ids being
-  // distinct -- are addressed with 32-bit offsets.
-  MOE_REQUIRE(T * (int64_t)I * 4 < ((int64_t)1 << 32), MOE_ERR_UNSUPPORTED, "%s: T*2I too large",
               who);
   MOE_REQUIRE((S == 0 || (d_gate_up && hidden_states && row_src)) && offsets && d_gate_up_proj,
               MOE_ERR_ARG, "%s: null pointer", who);

@@ -50,3 +50,38 @@ def test_routed_rows_beyond_4gib_match_halves():
         ref = a.float() + b.float()
         err = (full.float() - ref).abs().max() / ref.abs().max()
         assert err < 1e-2, float(err)
+
+
+@pytest.mark.parametrize("gemm", ["gate_up_dw", "down_dw_gathered"])
+def test_dw_expert_rows_beyond_4gib(gemm):
+    """Every token lists expert 0 in all K slots (accepted: the reference's
+    grouped_mm path does not require distinct ids), so expert 0 owns all
+    S = T*K routed rows and its k-major row operand -- d_gate_up [S, 2I] or
+    act_w [S, I] -- spans more than 4 GiB in one dW tile's k walk.  The
+    weight gradient must equal torch's fp32 product of the same bf16
+    operands (rows gathered through row_src) to the bf16 rounding of the
+    result; expert 1, with no rows, gets exact zeros."""
+    from moe_amd import ops
+    Hs, Is, Es, Ks = 256, 768, 2, 8
+    ld = 2 * Is if gemm == "gate_up_dw" else Is
+    Ts = ((1 << 32) // (ld * 2) + 4096) // Ks + 1
+    S = Ts * Ks
+    assert S * ld * 2 > 1 << 32
+    print(f"dW rows past 4 GiB: {gemm} T={Ts} S={S} ld={ld}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(5)
+    idx = torch.zeros(Ts, Ks, dtype=torch.int64, device=DEV)
+    plan = ops.permute(idx, Es)
+    a = torch.randn(S, ld, device=DEV, generator=g).to(torch.bfloat16)
+    rows = torch.randn(Ts, Hs, device=DEV, generator=g).to(torch.bfloat16)
+    tok = plan.row_src.long() // Ks
+    if gemm == "gate_up_dw":
+        dw = ops.gemm_gate_up_backward_dw(a, rows, plan, (Es, 2 * Is, Hs))
+        ref = a.float().t() @ rows[tok].float()            # [2I, H]
+    else:
+        dw = ops.gemm_down_backward_dw_gathered(rows, a, plan, (Es, Hs, Is))
+        ref = rows[tok].float().t() @ a.float()            # [H, I]
+    torch.cuda.synchronize()
+    err = ((dw[0].float() - ref).abs().max() / ref.abs().max()).item()
+    print(f"  max rel err {err:.2e}", flush=True)
+    assert err < 1e-2
+    assert not dw[1].any()
