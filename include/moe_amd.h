@@ -237,8 +237,12 @@ int moe_amd_permute_noalloc(const int64_t* topk_index, int64_t S, int E, int32_t
                             size_t tile_plan_bytes, void* stream);
 
 /* ------------------------------------------------------- grouped GEMMs */
-/* All GEMMs: bf16 operands (dtype = MOE_DTYPE_BF16), fp32 accumulation,
- * bf16 results; H and I must be multiples of 64; pointers 16-byte aligned.
+/* Grouped GEMMs: dtype MOE_DTYPE_BF16 (bf16 operands and results, fp32
+ * accumulation on the bf16 MFMA) or, for the entry points without "fused"
+ * or "gathered" in their name, MOE_DTYPE_F32 (fp32 operands and results on
+ * the fp32 MFMA: the XS-standard layer's precision); the fused and gathered
+ * backward entry points are bf16 only.  H and I must be multiples of 64;
+ * pointers 16-byte aligned.
  * The expert of each row tile is read from the tile plan on the device, so
  * empty and skewed experts cost no host synchronisation.  The kernels are
  * persistent: one workgroup per compute unit walks a contiguous range of
@@ -261,7 +265,12 @@ int moe_amd_gemm_down(const void* act, const int32_t* offsets, const void* tile_
 
 /* Backward of GEMM-2 w.r.t. its input fused with the SwiGLU backward:
  * d_act = dy @ down_proj[e]; (d_gate, d_up) from gate_up; writes
- * d_gate_up [S,2I].  Autograd of integrations/moe.py:447,457 (formula :226-242). */
+ * d_gate_up [S,2I].  Autograd of integrations/moe.py:447,457 (formula :226-242).
+ * With moe_amd_gemm_down_backward_dw and moe_amd_combine_backward this is
+ * the unfused backward chain (from a materialised dy): the fp32 layer's
+ * backward; in bf16 the layers take the fused pair below
+ * (moe_amd_gemm_down_backward_dx_fused, _dw_gathered), and the bf16 forms
+ * of these three serve callers that hold dy and the tests. */
 int moe_amd_gemm_down_backward_dx_dswiglu(const void* dy, const int32_t* offsets,
                                           const void* tile_plan, const void* down_proj,
                                           const void* gate_up, int64_t S, int E, int H, int I,
