@@ -1253,7 +1253,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
         }
         float my_w;
         int my_e;
-        group_sigmoid_topk<G, V>(sc, key, grp, g, K, p.ngroups, p.gtopk, p.renorm, p.scaling,
+        group_sigmoid_topk<G, V>(sc, key, grp, g, K, p.ngroups, p.gtopk, p.renorm, p.scaling, 0,
                                  tok && p.tpe != nullptr, scnt, my_w, my_e);
         if (tok) {
 #pragma unroll

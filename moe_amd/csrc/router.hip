@@ -100,17 +100,19 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void softmax_topk_kernel(
   }
 }
 
-// DeepSeek router (flat top-k, no expert groups) with G lanes per token, as
-// softmax_topk_group_kernel: scores = sigmoid(logits) stored, selection by
-// rank keys of the biased scores, the winner's unbiased score taken from its
-// owner lane (group max over the one lane that holds it), weights
-// renormalised by their sum in rank order (+1e-20), scaled, cast.  VEC: E ==
-// G*V, fp32 rows moved as 16-byte vectors.
+// DeepSeek router with G lanes per token, as softmax_topk_group_kernel:
+// scores = sigmoid(logits) stored, then the selection core shared with the
+// fused gating linear (router_group.h: group scores and kept groups when
+// ngroups > 0, each group on one lane; rank keys of the biased scores, the
+// winner's unbiased score taken from its owner lane, weights renormalised by
+// their sum in rank order (+1e-20), scaled), cast.  VEC: E == G*V, fp32 rows
+// moved as 16-byte vectors.
 template <int G, int V, bool VEC>
 __global__ __launch_bounds__(64 * kWavesPerBlock) void sigmoid_topk_group_kernel(
     const float* __restrict__ logits, const float* __restrict__ bias, int64_t T, int E, int K,
-    int renorm, float scaling, float* __restrict__ scores, void* __restrict__ topk_w,
-    int w_dtype, int64_t* __restrict__ topk_idx, float* __restrict__ tpe, int scores_in) {
+    int renorm, float scaling, int ngroups, int gtopk, float* __restrict__ scores,
+    void* __restrict__ topk_w, int w_dtype, int64_t* __restrict__ topk_idx,
+    float* __restrict__ tpe, int scores_in) {
   extern __shared__ int hist[];  // [E] when tpe != nullptr
   constexpr int TPW = 64 / G;
   const int lane = threadIdx.x & 63, g = lane & (G - 1), sub = lane / G;
@@ -120,6 +122,14 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void sigmoid_topk_group_kernel
     __syncthreads();
   }
   const int e0 = g * V;
+  // each entry's expert group (ngroups > 0), fixed per lane
+  int grp[V], cnt[V];
+  const int eg = ngroups > 0 ? E / ngroups : 1;
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    grp[j] = e0 + j < E ? (e0 + j) / eg : -1;
+    cnt[j] = 0;
+  }
   const int64_t stride = (int64_t)gridDim.x * kWavesPerBlock * TPW;
   for (int64_t tb = ((int64_t)blockIdx.x * kWavesPerBlock + wid) * TPW; tb < T; tb += stride) {
     const int64_t t = tb + sub;
@@ -154,28 +164,10 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void sigmoid_topk_group_kernel
       const int e = e0 + j;
       key[j] = e < E ? rank_key(sc[j] + (bias ? bias[e] : 0.0f), e) : 0ull;
     }
-    float my_w = 0.f, ssum = 0.f;
-    int my_e = 0;
-    for (int k = 0; k < K; ++k) {
-      uint64_t b = key[0];
-#pragma unroll
-      for (int j = 1; j < V; ++j) b = key[j] > b ? key[j] : b;
-      b = group_max_key<G>(b);
-      float own = -INFINITY;  // the winner's unbiased score, on its owner lane
-#pragma unroll
-      for (int j = 0; j < V; ++j) {
-        const bool hit = key[j] == b;
-        own = hit ? sc[j] : own;
-        key[j] = hit ? 0ull : key[j];
-      }
-      const float sk = group_max<G>(own);
-      ssum += sk;
-      if (g == k) {
-        my_w = sk;
-        my_e = key_index(b);
-      }
-    }
-    my_w = dsk_weight(my_w, ssum, renorm, scaling, scores_in);
+    float my_w;
+    int my_e;
+    group_sigmoid_topk<G, V>(sc, key, grp, g, K, ngroups, gtopk, renorm, scaling, scores_in,
+                             false, cnt, my_w, my_e);
     if (tok && g < K) {
       if (w_dtype == MOE_DTYPE_BF16)
         ((bf16*)topk_w)[t * K + g] = f2bf(my_w);
@@ -897,12 +889,15 @@ int sigmoid_topk_run(const float* logits, const float* expert_bias, int64_t T, i
   size_t shm = tokens_per_expert ? (size_t)E * sizeof(int) : 0;
   int G, V;
   group_shape(E, K, G, V);
-  if (num_groups <= 0 && G) {
+  // G lanes per token: flat top-k, or expert groups that each fit one lane's
+  // group score (num_groups <= G)
+  if (G && (num_groups <= 0 || num_groups <= G)) {
     hipStream_t st = (hipStream_t)stream;
     const bool vec = E == G * V && al16(logits) && al16(scores);
+    const int ng = num_groups > 0 ? num_groups : 0, gk = num_groups > 0 ? group_topk : 0;
 #define MOE_SIGMOID_GROUP(G_, V_, VEC_)                                                       \
   sigmoid_topk_group_kernel<G_, V_, VEC_><<<grid_group(T, G_), 64 * kWavesPerBlock, shm, st>>>( \
-      logits, expert_bias, T, E, K, renormalize, scaling_factor, scores, topk_weights,        \
+      logits, expert_bias, T, E, K, renormalize, scaling_factor, ng, gk, scores, topk_weights, \
       weights_dtype, topk_index, tokens_per_expert, scores_in)
 #define MOE_SIGMOID_GROUP_V(G_, V_)            \
   do {                                          \

@@ -95,8 +95,9 @@ __device__ __forceinline__ float dsk_weight(float v, float ssum, int renorm, flo
   return v;
 }
 
-// DeepSeek-V3 selection of one token on a group of G lanes (the gating
-// linear's fused epilogue, gemm.hip): lane g holds the token's entries
+// DeepSeek-V3 selection of one token on a group of G lanes (the router
+// kernel, router.hip, and the gating linear's fused epilogue, gemm.hip, so
+// that both produce the same bits): lane g holds the token's entries
 // e0 = g*V .. e0+V-1 as unbiased sigmoid scores sc and rank keys of the
 // biased scores (0 past E).  With ngroups > 0 the experts form ngroups equal
 // groups of eg = E/ngroups (ngroups <= G); each group is scored by the sum of
@@ -106,15 +107,16 @@ __device__ __forceinline__ float dsk_weight(float v, float ssum, int renorm, flo
 // max over the keys; the winner's owner lane hands its unbiased score to the
 // group (router.py:130) and counts the selection in cnt (when count), the
 // scores are summed in rank order for the renormalisation (+1e-20) and
-// lane g < K receives the g-th weight and expert (router.py:133-138).  The
-// order of every step is the one of the router kernels (router.hip), so the
-// selection and the weights are theirs bit for bit on the same scores.
+// lane g < K receives the g-th weight and expert (router.py:133-138), in
+// torch's bf16 arithmetic when scores_in (dsk_weight).  The order of every
+// step is that of the wave-per-token router kernel as well, so the
+// selection and the weights are its bit for bit on the same scores.
 template <int G, int V>
 __device__ __forceinline__ void group_sigmoid_topk(const float (&sc)[V], uint64_t (&key)[V],
                                                    const int (&grp)[V], int g, int K,
                                                    int ngroups, int gtopk, int renorm,
-                                                   float scaling, bool count, int (&cnt)[V],
-                                                   float& my_w, int& my_e) {
+                                                   float scaling, int scores_in, bool count,
+                                                   int (&cnt)[V], float& my_w, int& my_e) {
   if (ngroups > 0) {
     const int per = K / gtopk;
     float gv = -INFINITY;  // lane g < ngroups: group g's score
@@ -168,7 +170,7 @@ __device__ __forceinline__ void group_sigmoid_topk(const float (&sc)[V], uint64_
       my_e = key_index(b);
     }
   }
-  my_w = dsk_weight(my_w, ssum, renorm, scaling, 0);
+  my_w = dsk_weight(my_w, ssum, renorm, scaling, scores_in);
 }
 
 }  // namespace moe
