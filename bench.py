@@ -276,36 +276,64 @@ def copy_calibration(nbytes: int) -> None:
 # HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE and --pmc
 # WRITE_SIZE (one pass each) and scaled by the same counters on a plain copy of
 # known size (`--copy-calibration`); the commands and per-counter figures are
-# in profiles/gemm_hbm_traffic_L.md and profiles/retrofit_hbm_traffic.md.
+# in profiles/gemm_hbm_traffic_L.md and profiles/hbm_traffic_retrofit_XS_global_M.md.
 RECORDED_TRAFFIC = {
     "L": {
-        "gemm_gate_up_swiglu": 11617452787,
-        "gemm_down": 4745965057,
-        "gemm_down_backward_dx_fused": 7814923499,
-        "gemm_down_backward_dw_gathered": 4626583699,
-        "gemm_gate_up_backward_dx": 8857669989,
-        "gemm_gate_up_backward_dw": 7192684761,
-        "torch_gating_linear": 289694449,
-        "router_linear_backward_dx": 290641825,
-        "router_linear_backward_dw": 318965858,
+        "gemm_gate_up_swiglu": 11223408854,
+        "gemm_down": 4755817342,
+        "gemm_down_backward_dx_fused": 8402907650,
+        "gemm_down_backward_dw_gathered": 4656800124,
+        "gemm_gate_up_backward_dx": 8639176793,
+        "gemm_gate_up_backward_dw": 7346548871,
+        "torch_gating_linear": 289706073,
+        "router_linear_backward_dx": 290632197,
+        "router_linear_backward_dw": 318968879,
+        "combine": 2420155132,
+        "gather_backward": 2686439119,
     },
     "Retrofit": {
-        "gemm_gate_up_backward_dw": 12607157703,
-        "gemm_down_backward_dw_gathered": 6583395175,
-        "gemm_gate_up_swiglu": 4202210569,
-        "gemm_gate_up_backward_dx": 4098279500,
-        "gemm_down_backward_dx_fused": 3149835726,
-        "gemm_down": 2185717094,
-        "combine": 605131920,
-        "gather_backward": 604592386,
-        "router_sigmoid_topk": 236797195,
-        "router_sigmoid_topk_backward": 244219508,
+        "gemm_gate_up_swiglu": 4259894233,
+        "gemm_down": 2187627238,
+        "gemm_down_backward_dx_fused": 2953221848,
+        "gemm_down_backward_dw_gathered": 6584539798,
+        "gemm_gate_up_backward_dx": 4160436454,
+        "gemm_gate_up_backward_dw": 12601085429,
+        "combine": 605117922,
+        "gather_backward": 604582303,
+        "router_sigmoid_topk": 236798958,
+        "router_sigmoid_topk_backward": 236630583,
+    },
+    "XS global": {
+        "gemm_gate_up_swiglu": 988172263,
+        "gemm_down": 485318597,
+        "gemm_down_backward_dx_fused": 915755323,
+        "gemm_down_backward_dw_gathered": 460877930,
+        "gemm_gate_up_backward_dx": 841622096,
+        "gemm_gate_up_backward_dw": 765743919,
+        "torch_gating_linear": 40041486,
+        "router_linear_backward_dx": 40104928,
+        "router_linear_backward_dw": 71518478,
+        "combine": 168878452,
+        "gather_backward": 201893637,
+    },
+    "M standard": {
+        "gemm_gate_up_swiglu": 5298209282,
+        "gemm_down": 2585489976,
+        "gemm_down_backward_dx_fused": 4083282218,
+        "gemm_down_backward_dw_gathered": 2665683965,
+        "gemm_gate_up_backward_dx": 4752061988,
+        "gemm_gate_up_backward_dw": 4350178253,
+        "torch_gating_linear": 147061259,
+        "router_linear_backward_dx": 147699669,
+        "router_linear_backward_dw": 176370177,
+        "combine": 1210118315,
+        "gather_backward": 1343246294,
     },
 }
 
 
 def recorded_traffic(cfg_name: str, kernel: str):
-    """Measured HBM bytes per launch of `kernel` at the L or Retrofit shape, else None."""
+    """Measured HBM bytes per launch of `kernel` at a benchmark workload, else None."""
     for key, table in RECORDED_TRAFFIC.items():
         if cfg_name.startswith(key):
             return table.get(kernel)
