@@ -3,6 +3,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <atomic>
 #include <stdint.h>
 #include <stddef.h>
 
@@ -32,6 +33,21 @@ int check_launch(const char* what);
   } while (0)
 
 static inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Raises `kernel`'s dynamic-LDS limit to `bytes` on the current device the
+// first time it is launched there (`done` is that kernel's own per-device
+// record); later launches on the device make no call besides the launch.
+static inline hipError_t set_dynamic_lds_once(std::atomic<int> (&done)[64], const void* kernel,
+                                              int bytes) {
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return err;
+  const bool cached = dev >= 0 && dev < 64;
+  if (cached && done[dev].load(std::memory_order_acquire) >= bytes) return hipSuccess;
+  err = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (err == hipSuccess && cached) done[dev].store(bytes, std::memory_order_release);
+  return err;
+}
 
 // ---- GEMM tile plan (written by the permutation, read by the GEMMs) -----
 // int32 tile_starts[3][E+1]: exclusive prefix of ceil(count_e / BM) for the

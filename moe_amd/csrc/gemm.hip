@@ -1622,8 +1622,9 @@ int launch(const GemmArgs& a, int max_tiles, hipStream_t st) {
                          sizeof(bf16);
   const size_t lds = stages > staging ? stages : staging;
   if (max_tiles <= 0) return MOE_OK;
-  hipError_t err = hipFuncSetAttribute((const void*)grouped_gemm_kernel<MODE, BR>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  static std::atomic<int> lds_done[64];
+  hipError_t err =
+      set_dynamic_lds_once(lds_done, (const void*)grouped_gemm_kernel<MODE, BR>, (int)lds);
   if (err != hipSuccess) {
     set_error("grouped_gemm: hipFuncSetAttribute failed: %s", hipGetErrorString(err));
     return MOE_ERR_HIP;

@@ -360,8 +360,8 @@ template <int MODE>
 int launch_f32(const FArgs& a, int64_t blocks, hipStream_t st, const char* who) {
   if (blocks <= 0) return MOE_OK;
   MOE_REQUIRE(blocks < ((int64_t)1 << 31), MOE_ERR_UNSUPPORTED, "%s: too many tiles", who);
-  hipError_t err = hipFuncSetAttribute((const void*)f32_gemm_kernel<MODE>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsBytes);
+  static std::atomic<int> lds_done[64];
+  hipError_t err = set_dynamic_lds_once(lds_done, (const void*)f32_gemm_kernel<MODE>, (int)kLdsBytes);
   if (err != hipSuccess) {
     set_error("%s: hipFuncSetAttribute failed: %s", who, hipGetErrorString(err));
     return MOE_ERR_HIP;
