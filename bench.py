@@ -8,7 +8,10 @@ backward, routing-weight gradient reduction, GEMM-2 dW, GEMM-1 dW, router
 backward, gating-linear dW (split-K), GEMM-1 dX, gating-linear dX, gather +
 add), every kernel hand-written HIP.  Default
 workload: the L (Qwen3-30B-A3B) layer, T=65536, H=2048, E=128, K=8, I=768,
-bf16.
+bf16.  The expert weights' gradients: autograd's dense tensors, or (the
+global-bank workloads, by default) added in place into the weights'
+main_grad; either way the bank's gradient accumulates over the layer calls
+of one optimizer step (the config's bank_calls), as in training.
 
 Prints ONE JSON line on stdout (progress goes to stderr).  The line carries
 the layer throughput (tokens/s), per-kernel HIP-event timings over the timed
@@ -51,15 +54,18 @@ def gemm_flops(name: str, S: int, H: int, I: int) -> float:
         "moe_amd_gemm_gate_up_backward_dx": 2.0 * S * 2 * I * H,
         "moe_amd_gemm_gate_up_backward_dw": 2.0 * S * 2 * I * H,
     }
-    return per.get(name, 0.0)
+    return per.get(name.replace("_accumulate", ""), 0.0)
 
 
-def hbm_bytes(name: str, cfg) -> float:
+def hbm_bytes(name: str, cfg, touched: int | None = None) -> float:
     """Algorithmic HBM bytes of a launch: each operand read once (routed rows
-    as gathered, S*H), each output written once (b = element size)."""
+    as gathered, S*H), each output written once (b = element size); the
+    accumulating dW GEMMs read and write the gradients of the `touched`
+    experts (those with routed rows) only."""
     T, H, K, E, S, I = cfg.T, cfg.H, cfg.K, cfg.E, cfg.S, cfg.I
     b = 2 if cfg.dtype == torch.bfloat16 else 4
     w1, w2 = E * 2 * I * H * b, E * H * I * b
+    f = (E if touched is None else touched) / E
     per = {
         "moe_amd_combine": S * H * b + S * 8 + T * H * b,
         "moe_amd_combine_backward": T * H * b + 2 * S * H * b + S * 12,
@@ -75,6 +81,8 @@ def hbm_bytes(name: str, cfg) -> float:
         "moe_amd_gemm_down_backward_dw_gathered": S * H * b + S * I * b + w2,
         "moe_amd_gemm_gate_up_backward_dx": S * 2 * I * b + w1 + S * H * b,
         "moe_amd_gemm_gate_up_backward_dw": S * 2 * I * b + S * H * b + w1,
+        "moe_amd_gemm_down_backward_dw_gathered_accumulate": S * H * b + S * I * b + 2 * f * w2,
+        "moe_amd_gemm_gate_up_backward_dw_accumulate": S * 2 * I * b + S * H * b + 2 * f * w1,
     }
     return per.get(name, 0.0)
 
@@ -398,14 +406,14 @@ def routing_consumers(cfg, probs, dev, reps: int = 5) -> dict:
     return out
 
 
-def kernel_table(per: dict, cfg, steps: int, peak: float):
+def kernel_table(per: dict, cfg, steps: int, peak: float, touched: int):
     """Per-entry-point averages, FLOP/s and GB/s from recorded HIP events."""
     kernels = {}
     gemm_ms = gemm_fl = 0.0
     for name, ts in per.items():
         avg = sum(ts) / len(ts)
         fl = gemm_flops(name, cfg.S, cfg.H, cfg.I)
-        by = hbm_bytes(name, cfg)
+        by = hbm_bytes(name, cfg, touched)
         k = {"launches_per_step": len(ts) / steps, "avg_ms": round(avg, 4)}
         if fl:
             k["tflops"] = round(fl / avg / 1e9, 1)
@@ -435,6 +443,11 @@ def main():
     ap.add_argument("--cpu-tokens", type=int, default=0,
                     help="CPU-baseline sample (0: the whole batch, or 128 tokens for banks "
                          "over 2 GB)")
+    ap.add_argument("--weight-grads", default="auto", choices=("auto", "autograd", "main_grad"),
+                    help="expert-weight gradients as autograd's dense tensors, or added in place "
+                         "into the weights' main_grad (fused accumulation; experts without rows "
+                         "untouched); auto: main_grad for the global-bank workloads, whose bank "
+                         "gradient sums bank_calls layer calls per optimizer step")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--reference-points", action="store_true",
                     help="time hipBLASLt against the dense MFMA mode on the GEMMs' dense "
@@ -469,12 +482,29 @@ def main():
     wr = inp.w_router.clone().requires_grad_(True)
     w1 = inp.gate_up_proj.requires_grad_(True)
     w2 = inp.down_proj.requires_grad_(True)
-    params = (x, wr, w1, w2)
     backward = cfg.backward
+    weight_grads = args.weight_grads
+    if weight_grads == "auto":
+        weight_grads = ("main_grad" if backward and cfg.bank_calls > 1
+                        and cfg.dtype == torch.bfloat16 else "autograd")
+    if weight_grads == "main_grad":
+        w1.main_grad = torch.zeros_like(w1)
+        w2.main_grad = torch.zeros_like(w2)
+    calls = [0]
 
     def step():
-        for p in params:
-            p.grad = None
+        # One layer call of a training step.  The input and the router are
+        # the call's own; the expert bank's gradient sums the bank_calls calls
+        # of an optimizer step and is reset before every bank_calls-th call
+        # (main_grad zeroed; autograd's .grad dropped, so that the first call
+        # hands over its dW and the others add theirs, as in training).
+        x.grad = wr.grad = None
+        if calls[0] % cfg.bank_calls == 0:
+            if weight_grads == "main_grad":
+                w1.main_grad.zero_()
+                w2.main_grad.zero_()
+            w1.grad = w2.grad = None
+        calls[0] += 1
         out, probs, w, idx = moe_layer(x, wr, w1, w2, cfg.K, router=cfg.router,
                                        logit_offset=inp.logit_offset,
                                        expert_bias=inp.expert_bias, gating=args.gating)
@@ -491,6 +521,7 @@ def main():
     # HIP events between steps, on the stream every kernel is launched on
     # (torch's current stream), for the per-step median beside the mean.
     marks = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+    calls[0] = 0  # the timed steps start an optimizer step (main_grad zeroed first)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     marks[0].record()
@@ -509,6 +540,7 @@ def main():
     # so that each launch is timed alone; the timed steps above overlap the
     # gather backward with the weight-gradient GEMMs on a second stream).
     events: list = []
+    calls[0] = 0
     ops.record_kernel_times(events)
     torch.cuda.synchronize()
     k0 = time.perf_counter()
@@ -521,12 +553,13 @@ def main():
     for name, s_ev, e_ev in events:
         per.setdefault(name, []).append(s_ev.elapsed_time(e_ev))
     peak = PEAK_BF16_TFLOPS if cfg.dtype == torch.bfloat16 else PEAK_FP32_TFLOPS
-    kernels, gemm_ms, gemm_fl = kernel_table(per, cfg, args.kernel_steps, peak)
+    touched = int((torch.bincount(idx.reshape(-1), minlength=cfg.E) > 0).sum())
+    kernels, gemm_ms, gemm_fl = kernel_table(per, cfg, args.kernel_steps, peak, touched)
     gemms = {n: ts for n, ts in per.items() if gemm_flops(n, cfg.S, cfg.H, cfg.I)}
     dom = max(gemms, key=lambda n: sum(gemms[n]))
     dom_avg = sum(gemms[dom]) / len(gemms[dom])
     dom_fl = gemm_flops(dom, cfg.S, cfg.H, cfg.I)
-    dom_by = hbm_bytes(dom, cfg)
+    dom_by = hbm_bytes(dom, cfg, touched)
     # The dominant GEMM's bound: MFMA when its arithmetic intensity
     # (algorithmic FLOP per algorithmic HBM byte) exceeds the machine balance
     # peak / 8 TB/s, else HBM (the 1792-expert bank's weight gradients).
@@ -560,6 +593,9 @@ def main():
         "config": {"workload": f"{cfg.name} MoE layer {'fwd+bwd' if backward else 'fwd'}",
                    "T": cfg.T, "H": cfg.H, "E": cfg.E, "K": cfg.K, "I": cfg.I,
                    "router": cfg.router, "gating": args.gating,
+                   "weight_grads": weight_grads if backward else None,
+                   "bank_calls": cfg.bank_calls,
+                   "experts_with_rows": touched,
                    "load_imbalance_max_over_mean": round(imbalance, 3)},
         "gemm": {"flops_per_step": gemm_fl, "ms_per_step": round(gemm_ms, 4),
                  "tflops": round(gemm_fl / gemm_ms / 1e9, 1),

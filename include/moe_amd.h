@@ -317,6 +317,29 @@ int moe_amd_gemm_down_backward_dw_gathered(const void* d_out, const void* act_w,
                                            int64_t T, int64_t S, int E, int H, int I, int dtype,
                                            void* d_down_proj, void* stream);
 
+/* Fused gradient accumulation of the two dW GEMMs: d_down_proj[e] +=
+ * (moe_amd_gemm_down_backward_dw_gathered's d_down_proj[e]) and
+ * d_gate_up_proj[e] += (moe_amd_gemm_gate_up_backward_dw's) in place, bf16
+ * only, each element as torch adds two bf16 tensors (the GEMM result rounded
+ * to bf16, added in fp32, rounded to nearest even): the bits autograd's
+ * gradient accumulation gives.  Experts without routed rows are neither read
+ * nor written.  The tile plan is required (its dW schedule lists those
+ * experts last).  Replaces, for an expert bank shared by several layers
+ * (src/models/global_moe.py:138, :147-151), each layer's dense dW tensor plus
+ * the autograd accumulation that adds it to the bank's gradient (formula
+ * transformers/integrations/moe.py:226-242). */
+int moe_amd_gemm_down_backward_dw_gathered_accumulate(const void* d_out, const void* act_w,
+                                                      const int32_t* row_src, int top_k,
+                                                      const int32_t* offsets,
+                                                      const void* tile_plan, int64_t T, int64_t S,
+                                                      int E, int H, int I, int dtype,
+                                                      void* d_down_proj, void* stream);
+int moe_amd_gemm_gate_up_backward_dw_accumulate(const void* d_gate_up, const void* hidden_states,
+                                                const int32_t* row_src, int top_k,
+                                                const int32_t* offsets, const void* tile_plan,
+                                                int64_t T, int64_t S, int E, int H, int I,
+                                                int dtype, void* d_gate_up_proj, void* stream);
+
 /* d_xs = d_gate_up @ gate_up_proj[e]  ([S,H]). */
 int moe_amd_gemm_gate_up_backward_dx(const void* d_gate_up, const int32_t* offsets,
                                      const void* tile_plan, const void* gate_up_proj,

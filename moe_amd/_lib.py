@@ -72,6 +72,10 @@ SIGNATURES: dict[str, tuple] = {
     "moe_amd_gemm_gate_up_backward_dx": (_i, [_p, _p, _p, _p, _i64, _i, _i, _i, _i, _p, _p]),
     "moe_amd_gemm_gate_up_backward_dw": (
         _i, [_p, _p, _p, _i, _p, _p, _i64, _i64, _i, _i, _i, _i, _p, _p]),
+    "moe_amd_gemm_down_backward_dw_gathered_accumulate": (
+        _i, [_p, _p, _p, _i, _p, _p, _i64, _i64, _i, _i, _i, _i, _p, _p]),
+    "moe_amd_gemm_gate_up_backward_dw_accumulate": (
+        _i, [_p, _p, _p, _i, _p, _p, _i64, _i64, _i, _i, _i, _i, _p, _p]),
     "moe_amd_combine": (_i, [_p, _p, _p, _p, _i, _i64, _i, _i, _i, _i, _p, _p]),
     "moe_amd_combine_backward": (
         _i, [_p, _p, _p, _p, _p, _i, _i64, _i, _i, _i, _i, _p, _p, _p]),

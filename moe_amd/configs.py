@@ -29,6 +29,11 @@ class LayerConfig:
     zipf_s: float = 1.1
     bias_range: float = 0.0        # DeepSeek expert_bias ~ U(-r, r)
     backward: bool = True
+    # layer calls whose weight gradients sum into one bank gradient per
+    # optimizer step: the layers sharing a global bank x gradient-accumulation
+    # micro-batches (configs/scaling/xs_global.yaml: 16 layers, 1;
+    # retrofit_1.7b_global.yaml: 28 layers, 2); 1 for a per-layer bank
+    bank_calls: int = 1
 
     @property
     def S(self) -> int:
@@ -45,12 +50,13 @@ class LayerConfig:
 
 CONFIGS: dict[str, LayerConfig] = {
     "xs_std": LayerConfig("XS standard", 2048, 1024, 16, 4, 768, torch.float32, backward=False),
-    "xs_global": LayerConfig("XS global shared bank", 16384, 1024, 128, 4, 768, torch.bfloat16),
+    "xs_global": LayerConfig("XS global shared bank", 16384, 1024, 128, 4, 768, torch.bfloat16,
+                             bank_calls=16),
     "m_skew": LayerConfig("M standard, Zipf-skewed", 32768, 2048, 128, 8, 768, torch.bfloat16,
                           skew=2.0),
     "l": LayerConfig("L (Qwen3-30B-A3B)", 65536, 2048, 128, 8, 768, torch.bfloat16),
     "retrofit": LayerConfig("Retrofit 1.7B global bank", 16384, 2048, 1792, 8, 768,
-                            torch.bfloat16, router="sigmoid", bias_range=0.5),
+                            torch.bfloat16, router="sigmoid", bias_range=0.5, bank_calls=56),
 }
 
 

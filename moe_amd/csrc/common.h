@@ -69,11 +69,12 @@ static inline size_t plan_info_offset(int64_t S, int E, int b) {
 // Then the schedule of the two dW GEMMs (tiles of one expert cost its row
 // count): int32 queue[2][16] (per dW GEMM: the tile counters of 8 per-XCD
 // queues and a count of finished workgroups; zeroed by the permutation and
-// reset by each GEMM's last workgroup), int32 xstart[16] (experts of XCD x
-// are xorder[xstart[x] .. xstart[x+1]); 9 used), int32 xorder[E] (experts
+// reset by each GEMM's last workgroup), int32 xstart[32] (experts of XCD x
+// are xorder[xstart[x] .. xstart[x+1]), 9 used; at kSchedXnz + x the number
+// of them that have rows, which come first), int32 xorder[E] (experts
 // dealt to the XCDs heaviest first, in serpentine order).
 static inline size_t plan_sched_offset(int64_t S, int E) { return plan_info_offset(S, E, 3); }
-constexpr int kSchedQueueInts = 32, kSchedStartInts = 16;
+constexpr int kSchedQueueInts = 32, kSchedStartInts = 32, kSchedXnz = 16;
 static inline size_t plan_bytes(int64_t S, int E) {
   return plan_sched_offset(S, E) + align_up((size_t)(kSchedQueueInts + kSchedStartInts + E) * 4, 16);
 }

@@ -57,6 +57,7 @@
 // Reference: transformers/integrations/moe.py:439-459 (forward grouped_mm),
 // :226-242 (per-expert dX / dW formulas of the backward).
 #include <atomic>
+#include <type_traits>
 
 #include "common.h"
 #include "gemm_f32.h"
@@ -134,7 +135,18 @@ struct GemmArgs {
   int* queue;            // G2DW/G1DW: this GEMM's 8 XCD tile counters + finished count (null: static walk)
   const int* xstart;     // ... experts of XCD x: xorder[xstart[x] .. xstart[x+1])
   const int* xorder;
+  const int* xnz;        // ... of which the first xnz[x] have rows
+  int accumulate;        // G1DW/G2DWG: out[e] += dW[e] in place, experts without rows untouched
 };
+
+// Eight bf16 pairs added as torch adds two bf16 tensors: in fp32, then
+// rounded to nearest even.
+__device__ __forceinline__ u32x4 add_bf16x8(const u32x4& a, const u32x4& b) {
+  u32x4 r;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) r[w] = pack_bf2(bf_lo(a[w]) + bf_lo(b[w]), bf_hi(a[w]) + bf_hi(b[w]));
+  return r;
+}
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
@@ -275,7 +287,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       int v = -1;
       for (int k = 0; k < 8; ++k) {
         const int x = (xcd + k) & 7;
-        const int e0 = p.xstart[x], n = (p.xstart[x + 1] - e0) * per_e;
+        const int e0 = p.xstart[x], n = (p.accumulate ? p.xnz[x] : p.xstart[x + 1] - e0) * per_e;
         if (n == 0) continue;
         const int j = __hip_atomic_fetch_add(p.queue + x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (j < n) {
@@ -858,6 +870,42 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
   // unconditionally (rows and columns outside the output get an offset past
   // the descriptor's extent), so the next tile's first wait can leave
   // exactly these NST stores in flight.
+  // Fused accumulation (G1DW, G2DWG with p.accumulate): the destination of
+  // a tile's dW and the byte offsets of a lane's 32 pieces of 16 bytes in
+  // the order the epilogue stores them (two groups of 16, one per pair of
+  // 32-row sub-tiles); `pre` holds their old values.  Each group's 16 are
+  // loaded as the group starts, before its staging writes (measured faster
+  // than all 32 at the epilogue's start, or before the next tile's
+  // prologue).
+  constexpr bool ACCM = MODE == G1DW || MODE == G2DWG;
+  static_assert(!ACCM || TJ == 4, "accumulating epilogue: two groups of two sub-tiles");
+  auto dw_rsrc = [&](const Tile& c, int wd) {
+    const int ewr = wd >> 1, ewc = wd & 1;
+    if constexpr (MODE == G2DWG) {
+      const int o0 = c.ct * BC + ewc * 128;
+      const int no = min(128, H - o0);
+      return make_rsrc(p.out + (int64_t)c.e * H * I + (int64_t)o0 * I,
+                       no > 0 ? (uint32_t)no * (uint32_t)I * 2 : 0u);
+    } else {
+      const int r0 = c.row0 + ewr * WR;
+      const int nr = min(WR, I2 - r0);
+      return make_rsrc(p.out + (int64_t)c.e * I2 * H + (int64_t)r0 * H,
+                       nr > 0 ? (uint32_t)nr * (uint32_t)H * 2 : 0u);
+    }
+  };
+  auto dw_off = [&](const Tile& c, int ln, int wd, int j0, int it) -> uint32_t {
+    const int ewr = wd >> 1, ewc = wd & 1;
+    if constexpr (MODE == G2DWG) {
+      const int o = it * 8 + (ln >> 3), P = ln & 7;
+      const int col = c.row0 + ewr * WR + j0 * 32 + (P ^ ((o >> 1) & 7)) * 8;
+      return col < I ? (uint32_t)o * I * 2 + (uint32_t)col * 2 : kOOB;
+    } else {
+      const int rr = it * 4 + (ln >> 4), P = ln & 15;
+      const int col = c.ct * BC + ewc * 128 + (P ^ (rr & 15)) * 8, gr = j0 * 32 + rr;
+      return col < H ? (uint32_t)gr * H * 2 + (uint32_t)col * 2 : kOOB;
+    }
+  };
+  u32x4 pre[ACCM ? 32 : 1];
   auto epilogue_pf = [&](const Tile& c) {
     // lane- and wave-derived addresses formed here (opaque to the
     // optimizer, which would otherwise hoist them out of the tile loop)
@@ -1063,18 +1111,33 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       const int no = min(128, H - o0);
       const auto rs = make_rsrc(p.out + (int64_t)c.e * H * I + (int64_t)o0 * I,
                                 no > 0 ? (uint32_t)no * (uint32_t)I * 2 : 0u);
+      // accumulating: the old values (`pre`) are added in the store loop
+      auto body = [&](auto acc_t) {
+        constexpr bool ACC = decltype(acc_t)::value;
 #pragma unroll
-      for (int j0 = 0; j0 < TJ; j0 += 2) {
-        const int nj = TJ - j0 >= 2 ? 2 : 1;
-        write_rows(j0, nj);
+        for (int j0 = 0; j0 < TJ; j0 += 2) {
+          const int nj = TJ - j0 >= 2 ? 2 : 1;
+          if constexpr (ACC) {
 #pragma unroll
-        for (int it = 0; it < 16; ++it) {
-          const int o = it * 8 + (ln >> 3), P = ln & 7;
-          const u32x4 v = *(const __attribute__((address_space(3))) u32x4*)(reg + o * 128 + P * 16);
-          const int col = c.row0 + ewr * WR + j0 * 32 + (P ^ ((o >> 1) & 7)) * 8;
-          st16(rs, col < I ? (uint32_t)o * I * 2 + (uint32_t)col * 2 : kOOB, v);
+            for (int it = 0; it < 16; ++it)
+              pre[(j0 >> 1) * 16 + it] = __builtin_amdgcn_raw_buffer_load_b128(rs, dw_off(c, ln, wd, j0, it), 0, 0);
+          }
+          write_rows(j0, nj);
+#pragma unroll
+          for (int it = 0; it < 16; ++it) {
+            const int o = it * 8 + (ln >> 3), P = ln & 7;
+            u32x4 v = *(const __attribute__((address_space(3))) u32x4*)(reg + o * 128 + P * 16);
+            if constexpr (ACC) v = add_bf16x8(pre[(j0 >> 1) * 16 + it], v);
+            st16(rs, dw_off(c, ln, wd, j0, it), v);
+          }
+          __builtin_amdgcn_sched_barrier(0);
         }
-        __builtin_amdgcn_sched_barrier(0);
+      };
+      if constexpr (MODE == G2DWG) {
+        if (p.accumulate) body(std::true_type{});
+        else body(std::false_type{});
+      } else {
+        body(std::false_type{});
       }
     } else {
       // y (G2F), d_xs (G1DX): routed rows x H; the gating linear's d_x (RDX):
@@ -1093,18 +1156,38 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       const int nr = min(WR, nrows_all - r0);
       const auto rs = make_rsrc(ob + (int64_t)r0 * H, nr > 0 ? (uint32_t)nr * (uint32_t)H * 2 : 0u);
       const int cb = c.ct * BC + ewc * 128;
+      // G1DW accumulating: as G2DWG's above
+      auto body = [&](auto acc_t) {
+        constexpr bool ACC = decltype(acc_t)::value;
 #pragma unroll
-      for (int j0 = 0; j0 < TJ; j0 += 2) {
-        const int nj = TJ - j0 >= 2 ? 2 : 1;
-        write_rows(j0, nj);
+        for (int j0 = 0; j0 < TJ; j0 += 2) {
+          const int nj = TJ - j0 >= 2 ? 2 : 1;
+          if constexpr (ACC) {
 #pragma unroll
-        for (int it = 0; it < 8 * nj; ++it) {
-          const int rr = it * 4 + (ln >> 4), P = ln & 15;
-          const u32x4 v = *(const __attribute__((address_space(3))) u32x4*)(reg + rr * 256 + P * 16);
-          const int col = cb + (P ^ (rr & 15)) * 8, gr = j0 * 32 + rr;
-          st16(rs, col < H ? (uint32_t)gr * H * 2 + (uint32_t)col * 2 : kOOB, v);
+            for (int it = 0; it < 16; ++it)
+              pre[(j0 >> 1) * 16 + it] = __builtin_amdgcn_raw_buffer_load_b128(rs, dw_off(c, ln, wd, j0, it), 0, 0);
+          }
+          write_rows(j0, nj);
+#pragma unroll
+          for (int it = 0; it < 8 * nj; ++it) {
+            const int rr = it * 4 + (ln >> 4), P = ln & 15;
+            u32x4 v = *(const __attribute__((address_space(3))) u32x4*)(reg + rr * 256 + P * 16);
+            const int col = cb + (P ^ (rr & 15)) * 8, gr = j0 * 32 + rr;
+            uint32_t off = col < H ? (uint32_t)gr * H * 2 + (uint32_t)col * 2 : kOOB;
+            if constexpr (ACC) {
+              v = add_bf16x8(pre[(j0 >> 1) * 16 + it], v);
+              off = dw_off(c, ln, wd, j0, it);
+            }
+            st16(rs, off, v);
+          }
+          __builtin_amdgcn_sched_barrier(0);
         }
-        __builtin_amdgcn_sched_barrier(0);
+      };
+      if constexpr (MODE == G1DW) {
+        if (p.accumulate) body(std::true_type{});
+        else body(std::false_type{});
+      } else {
+        body(std::false_type{});
       }
     }
   };
@@ -1155,8 +1238,8 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       if (more) {
         nxt = decode(tn_next);
         setup(nxt);
-        if (nxt.nk > 0) prologue();
       }
+      if (more && nxt.nk > 0) prologue();
       epilogue_pf(cur);
       if (!more) break;
       take_rows();
@@ -2236,6 +2319,7 @@ void set_dw_schedule(GemmArgs& a, const void* tile_plan, int64_t S, int E, int w
   a.queue = sched + 16 * which;
   a.xstart = sched + kSchedQueueInts;
   a.xorder = sched + kSchedQueueInts + kSchedStartInts;
+  a.xnz = sched + kSchedQueueInts + kSchedXnz;
 }
 
 extern "C" int moe_amd_gemm_down_backward_dw(const void* dy, const void* act,
@@ -2271,13 +2355,12 @@ extern "C" int moe_amd_gemm_down_backward_dw(const void* dy, const void* act,
   return launch<G2DW, 256>(a, a.n_tiles, (hipStream_t)stream);
 }
 
-extern "C" int moe_amd_gemm_down_backward_dw_gathered(const void* d_out, const void* act_w,
-                                                      const int32_t* row_src, int top_k,
-                                                      const int32_t* offsets,
-                                                      const void* tile_plan, int64_t T, int64_t S,
-                                                      int E, int H, int I, int dtype,
-                                                      void* d_down_proj, void* stream) {
-  const char* who = "gemm_down_backward_dw_gathered";
+namespace {
+int down_dw_gathered(const void* d_out, const void* act_w, const int32_t* row_src, int top_k,
+                     const int32_t* offsets, const void* tile_plan, int64_t T, int64_t S, int E,
+                     int H, int I, int dtype, void* d_down_proj, bool accumulate, void* stream,
+                     const char* who) {
+  MOE_REQUIRE(!accumulate || tile_plan, MOE_ERR_ARG, "%s: needs the tile plan", who);
   int rc = check_common(S, E, H, I, dtype, who);
   if (rc) return rc;
   MOE_REQUIRE(top_k >= 1 && S == T * top_k, MOE_ERR_ARG, "%s: S != T*top_k", who);
@@ -2302,16 +2385,36 @@ extern "C" int moe_amd_gemm_down_backward_dw_gathered(const void* d_out, const v
   a.n_ct = (H + BC - 1) / BC;
   a.n_tiles = E * a.n_rt * a.n_ct;
   set_dw_schedule(a, tile_plan, S, E, 0);
+  a.accumulate = accumulate;
   return launch<G2DWG, 256>(a, a.n_tiles, (hipStream_t)stream);
 }
+}  // namespace
 
-extern "C" int moe_amd_gemm_gate_up_backward_dw(const void* d_gate_up, const void* hidden_states,
-                                                const int32_t* row_src, int top_k,
-                                                const int32_t* offsets, const void* tile_plan,
-                                                int64_t T, int64_t S, int E, int H, int I,
-                                                int dtype, void* d_gate_up_proj, void* stream) {
-  const char* who = "gemm_gate_up_backward_dw";
-  if (dtype == MOE_DTYPE_F32)
+extern "C" int moe_amd_gemm_down_backward_dw_gathered(const void* d_out, const void* act_w,
+                                                      const int32_t* row_src, int top_k,
+                                                      const int32_t* offsets,
+                                                      const void* tile_plan, int64_t T, int64_t S,
+                                                      int E, int H, int I, int dtype,
+                                                      void* d_down_proj, void* stream) {
+  return down_dw_gathered(d_out, act_w, row_src, top_k, offsets, tile_plan, T, S, E, H, I, dtype,
+                          d_down_proj, false, stream, "gemm_down_backward_dw_gathered");
+}
+
+extern "C" int moe_amd_gemm_down_backward_dw_gathered_accumulate(
+    const void* d_out, const void* act_w, const int32_t* row_src, int top_k,
+    const int32_t* offsets, const void* tile_plan, int64_t T, int64_t S, int E, int H, int I,
+    int dtype, void* d_down_proj, void* stream) {
+  return down_dw_gathered(d_out, act_w, row_src, top_k, offsets, tile_plan, T, S, E, H, I, dtype,
+                          d_down_proj, true, stream, "gemm_down_backward_dw_gathered_accumulate");
+}
+
+namespace {
+int gate_up_dw(const void* d_gate_up, const void* hidden_states, const int32_t* row_src,
+               int top_k, const int32_t* offsets, const void* tile_plan, int64_t T, int64_t S,
+               int E, int H, int I, int dtype, void* d_gate_up_proj, bool accumulate,
+               void* stream, const char* who) {
+  MOE_REQUIRE(!accumulate || tile_plan, MOE_ERR_ARG, "%s: needs the tile plan", who);
+  if (dtype == MOE_DTYPE_F32 && !accumulate)
     return f32_gate_up_dw((const float*)d_gate_up, (const float*)hidden_states, row_src, top_k,
                           offsets, T, S, E, H, I, (float*)d_gate_up_proj, (hipStream_t)stream);
   int rc = check_common(S, E, H, I, dtype, who);
@@ -2337,5 +2440,24 @@ extern "C" int moe_amd_gemm_gate_up_backward_dw(const void* d_gate_up, const voi
   a.n_ct = (H + BC - 1) / BC;
   a.n_tiles = E * a.n_rt * a.n_ct;
   set_dw_schedule(a, tile_plan, S, E, 1);
+  a.accumulate = accumulate;
   return launch<G1DW, 256>(a, a.n_tiles, (hipStream_t)stream);
+}
+}  // namespace
+
+extern "C" int moe_amd_gemm_gate_up_backward_dw(const void* d_gate_up, const void* hidden_states,
+                                                const int32_t* row_src, int top_k,
+                                                const int32_t* offsets, const void* tile_plan,
+                                                int64_t T, int64_t S, int E, int H, int I,
+                                                int dtype, void* d_gate_up_proj, void* stream) {
+  return gate_up_dw(d_gate_up, hidden_states, row_src, top_k, offsets, tile_plan, T, S, E, H, I,
+                    dtype, d_gate_up_proj, false, stream, "gemm_gate_up_backward_dw");
+}
+
+extern "C" int moe_amd_gemm_gate_up_backward_dw_accumulate(
+    const void* d_gate_up, const void* hidden_states, const int32_t* row_src, int top_k,
+    const int32_t* offsets, const void* tile_plan, int64_t T, int64_t S, int E, int H, int I,
+    int dtype, void* d_gate_up_proj, void* stream) {
+  return gate_up_dw(d_gate_up, hidden_states, row_src, top_k, offsets, tile_plan, T, S, E, H, I,
+                    dtype, d_gate_up_proj, true, stream, "gemm_gate_up_backward_dw_accumulate");
 }

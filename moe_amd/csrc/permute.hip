@@ -159,10 +159,13 @@ __global__ __launch_bounds__(64) void tile_info_kernel(const int* __restrict__ o
 }
 
 // Single block of 1024 threads: the dW-GEMM schedule.  Experts are sorted
-// by an estimate of their dW tile cost (rows + a fixed epilogue cost, in 64
-// log-spaced buckets, heaviest first; by expert id within a bucket), then
-// dealt to the 8 XCDs in serpentine order (0..7, 7..0, ...), which balances
-// the XCDs' sums.  Also zeroes the GEMMs' queue counters.
+// by an estimate of their dW tile cost (rows + a fixed epilogue cost, in 63
+// log-spaced buckets, heaviest first, and the experts without rows in a
+// 64th, last; by expert id within a bucket), then dealt to the 8 XCDs in
+// serpentine order (0..7, 7..0, ...), which balances the XCDs' sums.  Each
+// XCD's list therefore ends with its experts without rows; xnz[x] counts
+// the others (the accumulating dW GEMMs claim only those).  Also zeroes the
+// GEMMs' queue counters.
 __global__ __launch_bounds__(1024) void dw_schedule_kernel(const int* __restrict__ counts, int E,
                                                            int* __restrict__ queue,
                                                            int* __restrict__ xstart,
@@ -172,7 +175,7 @@ __global__ __launch_bounds__(1024) void dw_schedule_kernel(const int* __restrict
   if (tid < kSchedQueueInts) queue[tid] = 0;
   if (tid < 64) hist[tid] = 0;
   // Experts per XCD under serpentine dealing depend on E only.
-  if (tid < kSchedStartInts) {
+  if (tid < kSchedXnz) {
     const int rounds = E / 8, rem = E % 8;
     int acc = 0;
     for (int x = 0; x < 8 && x < tid; ++x) {
@@ -183,9 +186,10 @@ __global__ __launch_bounds__(1024) void dw_schedule_kernel(const int* __restrict
   }
   __syncthreads();
   auto bucket = [](int n) {
+    if (n == 0) return 63;             // no rows: last
     const float c = (float)n + 192.f;  // rows, plus about three k-steps of epilogue
     const int b = (int)(8.f * __log2f(c * (1.f / 192.f)));
-    return 63 - min(63, max(0, b));  // 0 = heaviest
+    return 62 - min(62, max(0, b));  // 0 = heaviest
   };
   for (int e = tid; e < E; e += blockDim.x) atomicAdd(&hist[bucket(counts[e])], 1);
   __syncthreads();
@@ -198,6 +202,14 @@ __global__ __launch_bounds__(1024) void dw_schedule_kernel(const int* __restrict
     }
   }
   __syncthreads();
+  // The nnz experts with rows take ranks 0..nnz-1; under the serpentine
+  // dealing XCD x receives nnz/8 of them, plus one if its lane in the last,
+  // partial round is below nnz % 8.
+  if (tid < 8) {
+    const int nnz = hist[63], rz = nnz / 8, mz = nnz % 8;
+    const int lane = (rz & 1) ? 7 - tid : tid;
+    xstart[kSchedXnz + tid] = rz + (lane < mz ? 1 : 0);
+  }
   // Rank of each expert, heaviest bucket first: its bucket's start plus the
   // number of lower-id experts in the same bucket -- a stable counting sort,
   // so every call writes the same schedule.  Experts go 1024 at a time (one

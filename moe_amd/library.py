@@ -60,6 +60,24 @@ def _empty_like_none(t: Tensor) -> Tensor:
     return t.new_empty(0)
 
 
+def _main_grad(weight: Tensor) -> Optional[Tensor]:
+    """The fused gradient-accumulation buffer of an expert weight: its
+    ``main_grad`` attribute (Megatron-LM's name for it), or None.  When set,
+    the layer's backward adds the weight's gradient into it in place (with
+    the bits autograd's accumulation would give) and hands autograd None for
+    the weight; experts without routed rows are not touched, so an expert
+    bank shared by several layers is never written whole.  bf16 weights and
+    a bf16, contiguous main_grad of the weight's shape on its device only."""
+    g = getattr(weight, "main_grad", None)
+    if g is None:
+        return None
+    if (not isinstance(g, Tensor) or weight.dtype != torch.bfloat16 or g.dtype != torch.bfloat16
+            or g.shape != weight.shape or g.device != weight.device or not g.is_contiguous()):
+        raise ValueError("main_grad: fused gradient accumulation takes a bf16 expert weight and "
+                         "a contiguous bf16 main_grad of its shape on its device")
+    return g
+
+
 # ------------------------------------------------------------------ experts
 
 def _saves_act_y(dtype: torch.dtype, save_for_backward: bool) -> bool:
@@ -150,14 +168,35 @@ def _experts_bwd_f32(d_out, x, w, w1, w2, gu, act, y, plan, need_x, need_w1, nee
     return d_x, dw, d_w1, d_w2
 
 
-@torch.library.custom_op(f"{_LIB}::experts_bwd", mutates_args=())
+def _dw_down(d_out, act_w, plan, down_proj, need, acc):
+    if not need:
+        return _empty_like_none(down_proj)
+    if acc is not None:
+        ops.gemm_down_backward_dw_gathered_accumulate(d_out, act_w, plan, acc)
+        return _empty_like_none(down_proj)
+    return ops.gemm_down_backward_dw_gathered(d_out, act_w, plan, down_proj.shape)
+
+
+def _dw_gate_up(d_gu, x, plan, gate_up_proj, need, acc):
+    if not need:
+        return _empty_like_none(gate_up_proj)
+    if acc is not None:
+        ops.gemm_gate_up_backward_dw_accumulate(d_gu, x, plan, acc)
+        return _empty_like_none(gate_up_proj)
+    return ops.gemm_gate_up_backward_dw(d_gu, x, plan, gate_up_proj.shape)
+
+
+@torch.library.custom_op(f"{_LIB}::experts_bwd", mutates_args=("acc_w1", "acc_w2"))
 def experts_bwd(d_out: Tensor, hidden_states: Tensor, top_k_weights: Tensor, gate_up_proj: Tensor,
                 down_proj: Tensor, gate_up: Tensor, act: Tensor, y: Tensor, counts: Tensor,
                 offsets: Tensor, row_src: Tensor, slot: Tensor, tile_plan: Tensor, need_x: bool,
-                need_w1: bool, need_w2: bool) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+                need_w1: bool, need_w2: bool, acc_w1: Optional[Tensor],
+                acc_w2: Optional[Tensor]) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     """(d_x, d_topk_weights, d_gate_up_proj, d_down_proj) (formulas
     integrations/moe.py:226-242).  bf16: the combine's backward runs fused
-    into GEMM-2's; fp32: the unfused chain on the saved act and y."""
+    into GEMM-2's; fp32: the unfused chain on the saved act and y.  With
+    acc_w1 / acc_w2 (bf16 only) the weight gradients are added into them in
+    place and returned empty."""
     T, K = top_k_weights.shape
     plan = _plan(counts, offsets, row_src, slot, tile_plan, gate_up_proj.shape[0], K, T)
     d_out = d_out.to(hidden_states.dtype).contiguous()
@@ -171,11 +210,9 @@ def experts_bwd(d_out: Tensor, hidden_states: Tensor, top_k_weights: Tensor, gat
             ops.gemm_gate_up_backward_dx(d_gu, plan, gate_up_proj), plan, None)
     else:
         d_x = _empty_like_none(hidden_states)
-    d_w2 = (ops.gemm_down_backward_dw_gathered(d_out, act_w, plan, down_proj.shape)
-            if need_w2 else _empty_like_none(down_proj))
+    d_w2 = _dw_down(d_out, act_w, plan, down_proj, need_w2, acc_w2)
     del act_w
-    d_w1 = (ops.gemm_gate_up_backward_dw(d_gu, hidden_states, plan, gate_up_proj.shape)
-            if need_w1 else _empty_like_none(gate_up_proj))
+    d_w1 = _dw_gate_up(d_gu, hidden_states, plan, gate_up_proj, need_w1, acc_w1)
     if join is not None:
         join()
     return d_x, dw, d_w1, d_w2
@@ -183,11 +220,13 @@ def experts_bwd(d_out: Tensor, hidden_states: Tensor, top_k_weights: Tensor, gat
 
 @experts_bwd.register_fake
 def _(d_out, hidden_states, top_k_weights, gate_up_proj, down_proj, gate_up, act, y, counts,
-      offsets, row_src, slot, tile_plan, need_x, need_w1, need_w2):
+      offsets, row_src, slot, tile_plan, need_x, need_w1, need_w2, acc_w1, acc_w2):
     return (torch.empty_like(hidden_states) if need_x else hidden_states.new_empty(0),
             torch.empty_like(top_k_weights),
-            torch.empty_like(gate_up_proj) if need_w1 else gate_up_proj.new_empty(0),
-            torch.empty_like(down_proj) if need_w2 else down_proj.new_empty(0))
+            torch.empty_like(gate_up_proj) if need_w1 and acc_w1 is None
+            else gate_up_proj.new_empty(0),
+            torch.empty_like(down_proj) if need_w2 and acc_w2 is None
+            else down_proj.new_empty(0))
 
 
 def _experts_setup(ctx, inputs, output):
@@ -197,16 +236,20 @@ def _experts_setup(ctx, inputs, output):
     # gradient is materialised for them.
     ctx.set_materialize_grads(False)
     ctx.save_for_backward(x, w, w1, w2, gu, act, y, counts, offsets, row_src, slot, tile_plan)
+    ctx.main_grads = (_main_grad(w1), _main_grad(w2))
 
 
 def _experts_backward(ctx, d_out, *unused):
     need_x, _, need_w, need_w1, need_w2 = ctx.needs_input_grad[:5]
     if d_out is None:
         return (None,) * 6
+    acc1, acc2 = ctx.main_grads
     d_x, d_w, d_w1, d_w2 = torch.ops.moe_amd.experts_bwd(
-        d_out, *ctx.saved_tensors, bool(need_x), bool(need_w1), bool(need_w2))
-    return (d_x if need_x else None, None, d_w if need_w else None, d_w1 if need_w1 else None,
-            d_w2 if need_w2 else None, None)
+        d_out, *ctx.saved_tensors, bool(need_x), bool(need_w1), bool(need_w2),
+        acc1 if need_w1 else None, acc2 if need_w2 else None)
+    return (d_x if need_x else None, None, d_w if need_w else None,
+            d_w1 if need_w1 and acc1 is None else None,
+            d_w2 if need_w2 and acc2 is None else None, None)
 
 
 torch.library.register_autograd(f"{_LIB}::experts_fwd", _experts_backward,
@@ -566,16 +609,17 @@ def _(x, w_router, gate_up_proj, down_proj, top_k, renormalize, logit_offset, sa
             x.new_empty(S if save_for_backward else 0, I2)) + _plan_fake(S, E, dev)
 
 
-@torch.library.custom_op(f"{_LIB}::moe_layer_bwd", mutates_args=())
+@torch.library.custom_op(f"{_LIB}::moe_layer_bwd", mutates_args=("acc_w1", "acc_w2"))
 def moe_layer_bwd(d_out: Optional[Tensor], d_probs: Optional[Tensor], d_w: Optional[Tensor],
                   x: Tensor, w_router: Tensor, gate_up_proj: Tensor, down_proj: Tensor,
                   gate_up: Tensor, probs: Tensor, w: Tensor, idx: Tensor, counts: Tensor,
                   offsets: Tensor, row_src: Tensor, slot: Tensor, tile_plan: Tensor,
-                  renormalize: bool, need_x: bool, need_wr: bool, need_w1: bool, need_w2: bool
+                  renormalize: bool, need_x: bool, need_wr: bool, need_w1: bool, need_w2: bool,
+                  acc_w1: Optional[Tensor], acc_w2: Optional[Tensor]
                   ) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     """(d_x, d_w_router, d_gate_up_proj, d_down_proj).  The combine backward
     runs fused into GEMM-2's; the gating linear's dX is added inside the
-    gather backward."""
+    gather backward.  acc_w1 / acc_w2: as for experts_bwd."""
     T, K = idx.shape
     plan = _plan(counts, offsets, row_src, slot, tile_plan, gate_up_proj.shape[0], K, T)
     if d_out is None:
@@ -593,11 +637,9 @@ def moe_layer_bwd(d_out: Optional[Tensor], d_probs: Optional[Tensor], d_w: Optio
         d_x, join = _gather_backward_beside(
             d_xs, plan, ops.router_linear_backward_dx(d_logits, w_router))
         del d_xs
-    d_w2 = (ops.gemm_down_backward_dw_gathered(d_out, act_w, plan, down_proj.shape)
-            if need_w2 else down_proj.new_empty(0))
+    d_w2 = _dw_down(d_out, act_w, plan, down_proj, need_w2, acc_w2)
     del act_w
-    d_w1 = (ops.gemm_gate_up_backward_dw(d_gu, x, plan, gate_up_proj.shape)
-            if need_w1 else gate_up_proj.new_empty(0))
+    d_w1 = _dw_gate_up(d_gu, x, plan, gate_up_proj, need_w1, acc_w1)
     d_wr = w_router.new_empty(0)
     if need_wr:
         d_wr = ops.router_linear_backward_dw(d_logits, x)
@@ -608,11 +650,14 @@ def moe_layer_bwd(d_out: Optional[Tensor], d_probs: Optional[Tensor], d_w: Optio
 
 @moe_layer_bwd.register_fake
 def _(d_out, d_probs, d_w, x, w_router, gate_up_proj, down_proj, gate_up, probs, w, idx, counts,
-      offsets, row_src, slot, tile_plan, renormalize, need_x, need_wr, need_w1, need_w2):
+      offsets, row_src, slot, tile_plan, renormalize, need_x, need_wr, need_w1, need_w2,
+      acc_w1, acc_w2):
     return (torch.empty_like(x) if need_x else x.new_empty(0),
             torch.empty_like(w_router) if need_wr else w_router.new_empty(0),
-            torch.empty_like(gate_up_proj) if need_w1 else gate_up_proj.new_empty(0),
-            torch.empty_like(down_proj) if need_w2 else down_proj.new_empty(0))
+            torch.empty_like(gate_up_proj) if need_w1 and acc_w1 is None
+            else gate_up_proj.new_empty(0),
+            torch.empty_like(down_proj) if need_w2 and acc_w2 is None
+            else down_proj.new_empty(0))
 
 
 def _layer_setup(ctx, inputs, output):
@@ -623,17 +668,20 @@ def _layer_setup(ctx, inputs, output):
     ctx.save_for_backward(x, w_router, gate_up_proj, down_proj, gu, probs, w, idx, counts,
                           offsets, row_src, slot, tile_plan)
     ctx.renormalize = renormalize
+    ctx.main_grads = (_main_grad(gate_up_proj), _main_grad(down_proj))
 
 
 def _layer_backward(ctx, d_out, d_probs, d_w, *unused):
     need_x, need_wr, need_w1, need_w2 = (bool(n) for n in ctx.needs_input_grad[:4])
     if d_out is None and d_probs is None and d_w is None:
         return (None,) * 9
+    acc1, acc2 = ctx.main_grads
     d_x, d_wr, d_w1, d_w2 = torch.ops.moe_amd.moe_layer_bwd(
         d_out, d_probs, d_w, *ctx.saved_tensors, ctx.renormalize, need_x, need_wr, need_w1,
-        need_w2)
-    return (d_x if need_x else None, d_wr if need_wr else None, d_w1 if need_w1 else None,
-            d_w2 if need_w2 else None, None, None, None, None, None)
+        need_w2, acc1 if need_w1 else None, acc2 if need_w2 else None)
+    return (d_x if need_x else None, d_wr if need_wr else None,
+            d_w1 if need_w1 and acc1 is None else None,
+            d_w2 if need_w2 and acc2 is None else None, None, None, None, None, None)
 
 
 torch.library.register_autograd(f"{_LIB}::moe_layer_fwd", _layer_backward,

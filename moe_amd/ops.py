@@ -555,13 +555,88 @@ def gemm_down_backward_dw_gathered(d_out, act_w, plan: RoutingPlan, down_proj_sh
     _need_cuda(d_out, act_w)
     d_out = _contig(d_out)
     E, H, I = down_proj_shape
+    _check_out_shape("gemm_down_backward_dw_gathered", down_proj_shape,
+                     _dw_shape("gemm_down_backward_dw_gathered", plan, act_w, d_out, False))
     S = plan.num_rows
-    dw = out if out is not None else torch.empty(E, H, I, device=d_out.device, dtype=d_out.dtype)
+    dw = _out_or_new(out, (E, H, I), d_out)
     _call("moe_amd_gemm_down_backward_dw_gathered", d_out.data_ptr(), act_w.data_ptr(),
           plan.row_src.data_ptr(), plan.top_k, plan.offsets.data_ptr(),
           plan.tile_plan.data_ptr() if scheduled else None, plan.num_tokens, S, E, H, I,
           _dtype_code(d_out.dtype), dw.data_ptr(), _stream(d_out))
     return dw
+
+
+def _dw_shape(name: str, plan: RoutingPlan, rows: torch.Tensor, tokens: torch.Tensor,
+              rows_first: bool) -> tuple[int, int, int]:
+    """The weight shape two dW-GEMM operands imply -- per-row operand
+    `rows` [S, n] and token operand `tokens` [T, m]: [E, n, m] (gate_up: n =
+    2I, m = H) or, rows_first False, [E, m, n] (down: m = H, n = I) -- after
+    checking them against the plan."""
+    if rows.dim() != 2 or tokens.dim() != 2 or rows.shape[0] != plan.num_rows \
+            or tokens.shape[0] != plan.num_tokens:
+        raise ValueError(f"{name}: operands of shapes {tuple(rows.shape)} and "
+                         f"{tuple(tokens.shape)} do not match the plan's {plan.num_rows} rows "
+                         f"and {plan.num_tokens} tokens")
+    n, m = rows.shape[1], tokens.shape[1]
+    return (plan.num_experts, n, m) if rows_first else (plan.num_experts, m, n)
+
+
+def _check_out_shape(name: str, shape, expect) -> None:
+    if tuple(shape) != tuple(expect):
+        raise ValueError(f"{name}: weight shape {tuple(shape)} does not match the operands' "
+                         f"{tuple(expect)}")
+
+
+def _out_or_new(out: torch.Tensor | None, shape, like: torch.Tensor) -> torch.Tensor:
+    """A dW GEMM's output: the caller's `out` (contiguous, of `shape`, like's
+    dtype and device) or a new tensor."""
+    if out is None:
+        return torch.empty(shape, device=like.device, dtype=like.dtype)
+    if tuple(out.shape) != tuple(shape) or out.dtype != like.dtype or out.device != like.device \
+            or not out.is_contiguous():
+        raise ValueError(f"out must be a contiguous {like.dtype} tensor of shape {tuple(shape)} "
+                         f"on {like.device}")
+    return out
+
+
+def _check_accumulator(acc: torch.Tensor, shape, like: torch.Tensor, name: str) -> None:
+    if acc.shape != torch.Size(shape) or acc.dtype != torch.bfloat16 or not acc.is_contiguous() \
+            or acc.device != like.device:
+        raise ValueError(f"{name}: the accumulator must be a contiguous bf16 tensor of shape "
+                         f"{tuple(shape)} on {like.device}, got {acc.dtype} "
+                         f"{tuple(acc.shape)} on {acc.device}")
+
+
+@on_tensor_device
+def gemm_down_backward_dw_gathered_accumulate(d_out, act_w, plan: RoutingPlan, acc: torch.Tensor):
+    """acc [E,H,I] += gemm_down_backward_dw_gathered(d_out, act_w, plan), in
+    place, with autograd's bf16 rounding (the GEMM result rounded to bf16,
+    then the bf16 add); experts without rows are not touched."""
+    _need_cuda(d_out, act_w)
+    d_out = _contig(d_out)
+    name = "gemm_down_backward_dw_gathered_accumulate"
+    E, H, I = _dw_shape(name, plan, act_w, d_out, False)
+    _check_accumulator(acc, (E, H, I), d_out, name)
+    _call("moe_amd_gemm_down_backward_dw_gathered_accumulate", d_out.data_ptr(),
+          act_w.data_ptr(), plan.row_src.data_ptr(), plan.top_k, plan.offsets.data_ptr(),
+          plan.tile_plan.data_ptr(), plan.num_tokens, plan.num_rows, E, H, I,
+          _dtype_code(d_out.dtype), acc.data_ptr(), _stream(d_out))
+    return acc
+
+
+@on_tensor_device
+def gemm_gate_up_backward_dw_accumulate(dgu, x, plan: RoutingPlan, acc: torch.Tensor):
+    """acc [E,2I,H] += gemm_gate_up_backward_dw(dgu, x, plan), in place, as
+    gemm_down_backward_dw_gathered_accumulate."""
+    _need_cuda(dgu, x)
+    name = "gemm_gate_up_backward_dw_accumulate"
+    E, I2, H = _dw_shape(name, plan, dgu, x, True)
+    _check_accumulator(acc, (E, I2, H), dgu, name)
+    _call("moe_amd_gemm_gate_up_backward_dw_accumulate", dgu.data_ptr(), x.data_ptr(),
+          plan.row_src.data_ptr(), plan.top_k, plan.offsets.data_ptr(),
+          plan.tile_plan.data_ptr(), plan.num_tokens, plan.num_rows, E, H, I2 // 2,
+          _dtype_code(dgu.dtype), acc.data_ptr(), _stream(dgu))
+    return acc
 
 
 @on_tensor_device
@@ -572,7 +647,11 @@ def gemm_down_backward_dw(dy, act, plan: RoutingPlan, down_proj_shape, out=None,
     _need_cuda(dy, act)
     E, H, I = down_proj_shape
     S = plan.num_rows
-    dw = out if out is not None else torch.empty(E, H, I, device=dy.device, dtype=dy.dtype)
+    if tuple(dy.shape) != (S, H) or tuple(act.shape) != (S, I) or E != plan.num_experts:
+        raise ValueError(f"gemm_down_backward_dw: d_y {tuple(dy.shape)} and act "
+                         f"{tuple(act.shape)} do not match the weight shape "
+                         f"{tuple(down_proj_shape)} and the plan's {S} rows")
+    dw = _out_or_new(out, (E, H, I), dy)
     _call("moe_amd_gemm_down_backward_dw", dy.data_ptr(), act.data_ptr(),
           plan.offsets.data_ptr(), plan.tile_plan.data_ptr() if scheduled else None, S, E, H, I,
           _dtype_code(dy.dtype), dw.data_ptr(), _stream(dy))
@@ -597,8 +676,10 @@ def gemm_gate_up_backward_dw(dgu, x, plan: RoutingPlan, gate_up_proj_shape, out=
     """d_gate_up_proj [E,2I,H]; ``scheduled`` as for gemm_down_backward_dw."""
     _need_cuda(dgu, x)
     E, I2, H = gate_up_proj_shape
+    _check_out_shape("gemm_gate_up_backward_dw", gate_up_proj_shape,
+                     _dw_shape("gemm_gate_up_backward_dw", plan, dgu, x, True))
     S = plan.num_rows
-    dw = out if out is not None else torch.empty(E, I2, H, device=dgu.device, dtype=dgu.dtype)
+    dw = _out_or_new(out, (E, I2, H), dgu)
     _call("moe_amd_gemm_gate_up_backward_dw", dgu.data_ptr(), x.data_ptr(),
           plan.row_src.data_ptr(), plan.top_k, plan.offsets.data_ptr(),
           plan.tile_plan.data_ptr() if scheduled else None, plan.num_tokens, S,

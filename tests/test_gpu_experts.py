@@ -357,25 +357,30 @@ def test_router_linear_backward_f32(T, H, E, need):
 
 
 def _sched_tables(plan, S, E):
-    """(queue[2][16], xstart[9], xorder[E]) read back from the tile plan."""
+    """(queue[2][16], xstart[9], xnz[8], xorder[E]) read back from the tile
+    plan."""
     raw = plan.tile_plan.cpu().numpy()
     off = (3 * (E + 1) * 4 + 15) // 16 * 16
     for bm in (64, 128, 256):
         off += 16 * ((S + bm - 1) // bm + E)
-    v = raw[off: off + 4 * (48 + E)].view(np.int32)
-    return v[:32].reshape(2, 16), v[32:41], v[48:48 + E]
+    v = raw[off: off + 4 * (64 + E)].view(np.int32)
+    return v[:32].reshape(2, 16), v[32:41], v[48:56], v[64:64 + E]
 
 
 def _check_sched(plan, S, E):
     """The dW schedule tables are well-formed: reset queue counters, every
-    expert once, balanced XCD ranges and the serpentine bound on the XCDs'
-    rows.  Returns the per-XCD rows."""
-    queue, xstart, xorder = _sched_tables(plan, S, E)
+    expert once, balanced XCD ranges, each XCD's experts with rows first
+    (xnz of them) and the serpentine bound on the XCDs' rows.  Returns the
+    per-XCD rows."""
+    queue, xstart, xnz, xorder = _sched_tables(plan, S, E)
     assert not queue.any()                       # reset after each launch
     assert sorted(xorder.tolist()) == list(range(E))
     n = np.diff(xstart)
     assert xstart[0] == 0 and xstart[8] == E and n.max() - n.min() <= 1
     counts = plan.counts.cpu().numpy()
+    for i in range(8):
+        lst = counts[xorder[xstart[i]:xstart[i + 1]]]
+        assert (lst[:xnz[i]] > 0).all() and not lst[xnz[i]:].any()
     load = [counts[xorder[xstart[i]:xstart[i + 1]]].sum() for i in range(8)]
     assert max(load) <= sum(load) / 8 + counts.max() + 1   # serpentine dealing bound
     return load

@@ -21,10 +21,17 @@ OPS = ["experts_fwd", "experts_bwd", "moe_layer_fwd", "moe_layer_bwd", "router_l
        "sigmoid_topk_backward"]
 
 
+# The backward ops' optional fused-accumulation buffers (a weight's
+# main_grad) are their only mutable arguments; every other op is functional.
+ACCUMULATORS = {"experts_bwd": {"acc_w1", "acc_w2"}, "moe_layer_bwd": {"acc_w1", "acc_w2"}}
+
+
 @pytest.mark.parametrize("name", OPS)
 def test_registered_functional(name):
     op = getattr(torch.ops.moe_amd, name).default
-    assert not op._schema.is_mutable
+    mutable = {a.name for a in op._schema.arguments if a.alias_info and a.alias_info.is_write}
+    assert mutable == ACCUMULATORS.get(name, set())
+    assert all(not r.alias_info for r in op._schema.returns)
 
 
 def _inputs(T=96, H=128, E=8, K=2, I=64):
@@ -54,9 +61,15 @@ def test_fake_shapes():
         assert actf.dtype == torch.float32  # fp32 saves act and y for its unfused backward
         dx, dw, dw1, dw2 = torch.ops.moe_amd.experts_bwd(
             out, x, w, w1, w2, gu, act, y, counts, offsets, row_src, slot, plan, True, False,
-            True)
+            True, None, None)
         assert dx.shape == x.shape and dw.shape == w.shape and dw1.numel() == 0
         assert dw2.shape == w2.shape
+        # with fused accumulation buffers the weight gradients come back empty
+        acc1, acc2 = torch.empty_like(w1), torch.empty_like(w2)
+        _, _, dw1, dw2 = torch.ops.moe_amd.experts_bwd(
+            out, x, w, w1, w2, gu, act, y, counts, offsets, row_src, slot, plan, True, True,
+            True, acc1, acc2)
+        assert dw1.numel() == 0 and dw2.numel() == 0
         wr = torch.empty(E, H, dtype=torch.bfloat16)
         res = torch.ops.moe_amd.moe_layer_fwd(x, wr, w1, w2, K, True, None, True, "hip")
         assert [tuple(r.shape) for r in res[:5]] == [(T, H), (T, E), (T, K), (T, K), (S, 2 * I)]
