@@ -306,6 +306,8 @@ RECORDED_TRAFFIC = {
         "gemm_down_backward_dw_gathered": 6584539798,
         "gemm_gate_up_backward_dx": 4160436454,
         "gemm_gate_up_backward_dw": 12601085429,
+        "gemm_down_backward_dw_gathered_accumulate": 3221565168,
+        "gemm_gate_up_backward_dw_accumulate": 5932094247,
         "combine": 605117922,
         "gather_backward": 604582303,
         "router_sigmoid_topk": 236798958,
@@ -318,6 +320,8 @@ RECORDED_TRAFFIC = {
         "gemm_down_backward_dw_gathered": 460877930,
         "gemm_gate_up_backward_dx": 841622096,
         "gemm_gate_up_backward_dw": 765743919,
+        "gemm_down_backward_dw_gathered_accumulate": 667508511,
+        "gemm_gate_up_backward_dw_accumulate": 1205827387,
         "torch_gating_linear": 40041486,
         "router_linear_backward_dx": 40104928,
         "router_linear_backward_dw": 71518478,
