@@ -2041,9 +2041,18 @@ __global__ void reduce_chunks_kernel(const float* __restrict__ part, int nchunk,
   const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
   if (i >= n) return;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int c = 0; c < nchunk; ++c)
-    for (int h = 0; h < halves; ++h)
-      acc += *(const f32x4*)(part + ((int64_t)c * halves + h) * n + i);
+  // eight partials loaded together, then added in chunk order (the loads of
+  // a chunk-at-a-time loop each waited for the previous add)
+  const int np = nchunk * halves;
+  int c = 0;
+  for (; c + 8 <= np; c += 8) {
+    f32x4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = *(const f32x4*)(part + (int64_t)(c + u) * n + i);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc += v[u];
+  }
+  for (; c < np; ++c) acc += *(const f32x4*)(part + (int64_t)c * n + i);
   u32x2 w = {pack_bf2(acc[0], acc[1]), pack_bf2(acc[2], acc[3])};
   *(u32x2*)(out + i) = w;
 }
