@@ -310,11 +310,12 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
   struct Tile {
     int e, row0, row_end, ct, kbeg, kend, nk;
   };
-  auto decode = [&](int tt) {
+  // pre (token modes): the tile's {expert, first row, end row} loaded ahead
+  auto decode = [&](int tt, const int4* pre = nullptr) {
     Tile d;
     if constexpr (TOKEN) {
       d.ct = tt % p.n_ct;
-      const int4 ti = p.tile_info[tt / p.n_ct];
+      const int4 ti = pre ? *pre : p.tile_info[tt / p.n_ct];
       d.e = ti.x;
       d.row0 = ti.y;
       d.row_end = ti.z;
@@ -433,7 +434,9 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
   int nsrc[TOKEN ? TJ : 1], csrc[TOKEN ? TJ : 1];
   uint32_t cwr[TOKEN ? TJ : 1];
 
-  auto setup = [&](const Tile& d) {
+  // rs (gathered rows): the row_src entries of the lane's DMA rows, loaded
+  // ahead by rows_load
+  auto setup = [&](const Tile& d, const int* rs = nullptr) {
     kb_cur = d.kbeg;
     ke_cur = d.kend;
     nk_cur = d.nk;
@@ -521,7 +524,7 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       for (int i = 0; i < RPW; ++i) {
         const int f = kc_feature(wid + NW * i);
         const int r = min(d.row0 + f, d.row_end - 1);
-        const int tok = div_topk(p.row_src[r], p.tok_mul, p.tok_shift);
+        const int tok = div_topk(rs ? rs[i] : p.row_src[r], p.tok_mul, p.tok_shift);
         roff[i] = (uint32_t)tok * (uint32_t)(H * 2) + kc_chunk(f) * 16;
       }
       rstep = BK * 2;
@@ -555,6 +558,15 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
 #pragma unroll
       for (int j = 0; j < TJ; ++j)
         nsrc[j] = p.row_src[min(d.row0 + wr * WR + j * 32 + l32, d.row_end - 1)];
+    }
+  };
+
+  // The row_src entries setup() reads for a gathered-row tile (G1F, G2DXF).
+  auto rows_load = [&](const Tile& d, int (&rs)[GROW ? RPW : 1]) {
+    if constexpr (GROW) {
+#pragma unroll
+      for (int i = 0; i < RPW; ++i)
+        rs[i] = p.row_src[min(d.row0 + kc_feature(wid + NW * i), d.row_end - 1)];
     }
   };
 
@@ -1212,10 +1224,29 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
         }
       }
     };
+    // Token modes (static walk): the {expert, first row, end row} of the
+    // next two tiles (ti1, ti2) and, for gathered rows, the row_src entries
+    // of the next tile's DMA rows (rs1) are loaded a hand-over ahead, before
+    // that hand-over's prologue DMA (so that no wait of the main loop counts
+    // them), and the hand-over itself waits on no memory.
+    constexpr bool PRE = TOKEN;
+    int4 ti1 = make_int4(0, 0, 0, 0), ti2 = ti1;
+    int rs1[GROW ? RPW : 1];
+    auto ti_load = [&](int tt) -> int4 {
+      return tt < t_end ? p.tile_info[tt / p.n_ct] : make_int4(0, 0, 0, 0);
+    };
+    auto ahead = [&](int tt) {  // rs1 <- tile tt's rows (its info in ti1), ti2 <- the next info
+      if (tt < t_end) rows_load(decode(tt, &ti1), rs1);
+      ti2 = ti_load(tt + nslot);
+    };
     // (a dynamic walk may find no tile at all; every workgroup still
     // reaches the finished-count update below)
     Tile cur = decode(dyn ? max(t, 0) : t);
     if (dyn ? t >= 0 : t < t_end) setup(cur);
+    if constexpr (PRE) {
+      ti1 = ti_load(t + nslot);
+      ahead(t + nslot);
+    }
     if ((dyn ? t >= 0 : t < t_end) && cur.nk > 0) prologue();
     if (dyn ? t >= 0 : t < t_end) take_rows();
     bool first = true;
@@ -1236,8 +1267,15 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
       const bool more = dyn ? tn_next >= 0 : tn_next < t_end;
       Tile nxt = cur;
       if (more) {
-        nxt = decode(tn_next);
-        setup(nxt);
+        if constexpr (PRE) {
+          nxt = decode(tn_next, &ti1);
+          setup(nxt, rs1);
+          ti1 = ti2;
+          ahead(tn_next + nslot);
+        } else {
+          nxt = decode(tn_next);
+          setup(nxt);
+        }
       }
       if (more && nxt.nk > 0) prologue();
       epilogue_pf(cur);
