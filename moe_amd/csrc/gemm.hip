@@ -885,10 +885,11 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
   // Fused accumulation (G1DW, G2DWG with p.accumulate): the destination of
   // a tile's dW and the byte offsets of a lane's 32 pieces of 16 bytes in
   // the order the epilogue stores them (two groups of 16, one per pair of
-  // 32-row sub-tiles); `pre` holds their old values.  Each group's 16 are
-  // loaded as the group starts, before its staging writes (measured faster
-  // than all 32 at the epilogue's start, or before the next tile's
-  // prologue).
+  // 32-row sub-tiles); `pre` holds their old values, loaded eight pieces
+  // ahead of their use: the first eight before the staging writes, then one
+  // per stored piece (as fast as loading each group's 16 at its start, with
+  // 36 fewer VGPRs; all 32 at the epilogue's start, or before the next
+  // tile's prologue, measured 4% and 2% slower).
   constexpr bool ACCM = MODE == G1DW || MODE == G2DWG;
   static_assert(!ACCM || TJ == 4, "accumulating epilogue: two groups of two sub-tiles");
   auto dw_rsrc = [&](const Tile& c, int wd) {
@@ -1130,14 +1131,21 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
         for (int j0 = 0; j0 < TJ; j0 += 2) {
           const int nj = TJ - j0 >= 2 ? 2 : 1;
           if constexpr (ACC) {
+            if (j0 == 0) {
 #pragma unroll
-            for (int it = 0; it < 16; ++it)
-              pre[(j0 >> 1) * 16 + it] = __builtin_amdgcn_raw_buffer_load_b128(rs, dw_off(c, ln, wd, j0, it), 0, 0);
+              for (int k = 0; k < 8; ++k)
+                pre[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, dw_off(c, ln, wd, 0, k), 0, 0);
+            }
           }
           write_rows(j0, nj);
 #pragma unroll
           for (int it = 0; it < 16; ++it) {
             const int o = it * 8 + (ln >> 3), P = ln & 7;
+            if constexpr (ACC) {
+              const int kn = (j0 >> 1) * 16 + it + 8;
+              if (kn < 32)
+                pre[kn] = __builtin_amdgcn_raw_buffer_load_b128(rs, dw_off(c, ln, wd, (kn >> 4) * 2, kn & 15), 0, 0);
+            }
             u32x4 v = *(const __attribute__((address_space(3))) u32x4*)(reg + o * 128 + P * 16);
             if constexpr (ACC) v = add_bf16x8(pre[(j0 >> 1) * 16 + it], v);
             st16(rs, dw_off(c, ln, wd, j0, it), v);
@@ -1175,14 +1183,21 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
         for (int j0 = 0; j0 < TJ; j0 += 2) {
           const int nj = TJ - j0 >= 2 ? 2 : 1;
           if constexpr (ACC) {
+            if (j0 == 0) {
 #pragma unroll
-            for (int it = 0; it < 16; ++it)
-              pre[(j0 >> 1) * 16 + it] = __builtin_amdgcn_raw_buffer_load_b128(rs, dw_off(c, ln, wd, j0, it), 0, 0);
+              for (int k = 0; k < 8; ++k)
+                pre[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, dw_off(c, ln, wd, 0, k), 0, 0);
+            }
           }
           write_rows(j0, nj);
 #pragma unroll
           for (int it = 0; it < 8 * nj; ++it) {
             const int rr = it * 4 + (ln >> 4), P = ln & 15;
+            if constexpr (ACC) {
+              const int kn = (j0 >> 1) * 16 + it + 8;
+              if (kn < 32)
+                pre[kn] = __builtin_amdgcn_raw_buffer_load_b128(rs, dw_off(c, ln, wd, (kn >> 4) * 2, kn & 15), 0, 0);
+            }
             u32x4 v = *(const __attribute__((address_space(3))) u32x4*)(reg + rr * 256 + P * 16);
             const int col = cb + (P ^ (rr & 15)) * 8, gr = j0 * 32 + rr;
             uint32_t off = col < H ? (uint32_t)gr * H * 2 + (uint32_t)col * 2 : kOOB;
