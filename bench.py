@@ -287,17 +287,17 @@ def copy_calibration(nbytes: int) -> None:
 # in profiles/gemm_hbm_traffic_L.md and profiles/hbm_traffic_retrofit_XS_global_M.md.
 RECORDED_TRAFFIC = {
     "L": {
-        "gemm_gate_up_swiglu": 11223408854,
-        "gemm_down": 4755817342,
-        "gemm_down_backward_dx_fused": 8402907650,
-        "gemm_down_backward_dw_gathered": 4656800124,
-        "gemm_gate_up_backward_dx": 8639176793,
-        "gemm_gate_up_backward_dw": 7346548871,
-        "torch_gating_linear": 289706073,
-        "router_linear_backward_dx": 290632197,
-        "router_linear_backward_dw": 318968879,
-        "combine": 2420155132,
-        "gather_backward": 2686439119,
+        "gemm_gate_up_swiglu": 11724022260,
+        "gemm_down": 4744795525,
+        "gemm_down_backward_dx_fused": 8253627728,
+        "gemm_down_backward_dw_gathered": 4596779959,
+        "gemm_gate_up_backward_dx": 8668277529,
+        "gemm_gate_up_backward_dw": 7097372741,
+        "torch_gating_linear": 289691204,
+        "router_linear_backward_dx": 290595429,
+        "router_linear_backward_dw": 318972910,
+        "combine": 2420153756,
+        "gather_backward": 2686437232,
     },
     "Retrofit": {
         "gemm_gate_up_swiglu": 4259894233,
