@@ -201,6 +201,8 @@ def experts_bwd(d_out: Tensor, hidden_states: Tensor, top_k_weights: Tensor, gat
     plan = _plan(counts, offsets, row_src, slot, tile_plan, gate_up_proj.shape[0], K, T)
     d_out = d_out.to(hidden_states.dtype).contiguous()
     if hidden_states.dtype == torch.float32:
+        if acc_w1 is not None or acc_w2 is not None:
+            raise ValueError("experts_bwd: fused gradient accumulation takes bf16 layers only")
         return _experts_bwd_f32(d_out, hidden_states, top_k_weights.contiguous(), gate_up_proj,
                                 down_proj, gate_up, act, y, plan, need_x, need_w1, need_w2)
     d_gu, act_w, dw = ops.gemm_down_backward_fused(d_out, plan, down_proj, gate_up, top_k_weights)

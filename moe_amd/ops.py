@@ -553,7 +553,7 @@ def gemm_down_backward_dw_gathered(d_out, act_w, plan: RoutingPlan, down_proj_sh
     gemm_down_backward_fused's output.  ``scheduled`` as for
     gemm_down_backward_dw."""
     _need_cuda(d_out, act_w)
-    d_out = _contig(d_out)
+    d_out, act_w = _contig(d_out), _contig(act_w)
     E, H, I = down_proj_shape
     _check_out_shape("gemm_down_backward_dw_gathered", down_proj_shape,
                      _dw_shape("gemm_down_backward_dw_gathered", plan, act_w, d_out, False))
@@ -572,6 +572,8 @@ def _dw_shape(name: str, plan: RoutingPlan, rows: torch.Tensor, tokens: torch.Te
     `rows` [S, n] and token operand `tokens` [T, m]: [E, n, m] (gate_up: n =
     2I, m = H) or, rows_first False, [E, m, n] (down: m = H, n = I) -- after
     checking them against the plan."""
+    if rows.dtype != tokens.dtype:
+        raise TypeError(f"{name}: operands of dtypes {rows.dtype} and {tokens.dtype}")
     if rows.dim() != 2 or tokens.dim() != 2 or rows.shape[0] != plan.num_rows \
             or tokens.shape[0] != plan.num_tokens:
         raise ValueError(f"{name}: operands of shapes {tuple(rows.shape)} and "
@@ -613,7 +615,7 @@ def gemm_down_backward_dw_gathered_accumulate(d_out, act_w, plan: RoutingPlan, a
     place, with autograd's bf16 rounding (the GEMM result rounded to bf16,
     then the bf16 add); experts without rows are not touched."""
     _need_cuda(d_out, act_w)
-    d_out = _contig(d_out)
+    d_out, act_w = _contig(d_out), _contig(act_w)
     name = "gemm_down_backward_dw_gathered_accumulate"
     E, H, I = _dw_shape(name, plan, act_w, d_out, False)
     _check_accumulator(acc, (E, H, I), d_out, name)
@@ -629,6 +631,7 @@ def gemm_gate_up_backward_dw_accumulate(dgu, x, plan: RoutingPlan, acc: torch.Te
     """acc [E,2I,H] += gemm_gate_up_backward_dw(dgu, x, plan), in place, as
     gemm_down_backward_dw_gathered_accumulate."""
     _need_cuda(dgu, x)
+    dgu, x = _contig(dgu), _contig(x)
     name = "gemm_gate_up_backward_dw_accumulate"
     E, I2, H = _dw_shape(name, plan, dgu, x, True)
     _check_accumulator(acc, (E, I2, H), dgu, name)
@@ -675,6 +678,7 @@ def gemm_gate_up_backward_dw(dgu, x, plan: RoutingPlan, gate_up_proj_shape, out=
                              scheduled: bool = True):
     """d_gate_up_proj [E,2I,H]; ``scheduled`` as for gemm_down_backward_dw."""
     _need_cuda(dgu, x)
+    dgu, x = _contig(dgu), _contig(x)
     E, I2, H = gate_up_proj_shape
     _check_out_shape("gemm_gate_up_backward_dw", gate_up_proj_shape,
                      _dw_shape("gemm_gate_up_backward_dw", plan, dgu, x, True))

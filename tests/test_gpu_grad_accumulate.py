@@ -82,7 +82,8 @@ def test_dw_accumulate_matches_autograd_add(T, H, E, K, I, skew, active):
 
 
 def test_dw_accumulate_rejects():
-    """bf16 accumulators of the weight's shape only; a plan is required."""
+    """bf16, contiguous accumulators of the operands' weight shape only, and
+    operands that match the plan and each other."""
     T, H, E, K, I = 64, 128, 8, 2, 64
     idx = _routing(T, E, K, 1).to(DEV)
     plan = ops.permute(idx, E)
@@ -93,6 +94,11 @@ def test_dw_accumulate_rejects():
                 torch.zeros(E, H, 2 * I, dtype=BF, device=DEV).transpose(1, 2)):  # layout
         with pytest.raises(ValueError, match="accumulator"):
             ops.gemm_gate_up_backward_dw_accumulate(dgu, x, plan, acc)
+    acc = torch.zeros(E, 2 * I, H, dtype=BF, device=DEV)
+    with pytest.raises(TypeError, match="dtypes"):                       # operand dtypes
+        ops.gemm_gate_up_backward_dw_accumulate(dgu, x.float(), plan, acc)
+    with pytest.raises(ValueError, match="plan"):                        # operand rows
+        ops.gemm_gate_up_backward_dw_accumulate(dgu[:-1], x, plan, acc)
 
 
 def _bank(E, H, I, seed):
