@@ -205,14 +205,16 @@ def test_shared_bank_accumulates_gradients_across_layers():
 
 
 @pytest.mark.gpu
-def test_global_bank_dispatches_through_experts_interface():
+@pytest.mark.parametrize("main_grad", [False, True])
+def test_global_bank_dispatches_through_experts_interface(main_grad):
     """The global shared bank as the reference builds it (src/models/
     global_moe.py:45-66, :130-151), from transformers classes only: one
     Qwen3MoeExperts owned by a Qwen3MoeModel and called by two router-only
     blocks (a Qwen3MoeTopKRouter each).  After hf.install() both calls
     dispatch through the "mi355x" ExpertsInterface key (counted), the gates
     are the HIP routers, and the bank's dW is the oracle's sum over both
-    calls."""
+    calls -- in .grad, or, with main_grad buffers on the bank's two
+    parameters, accumulated in place into them with .grad left None."""
     import copy
     from unittest import mock
     from transformers import Qwen3MoeConfig
@@ -257,6 +259,9 @@ def test_global_bank_dispatches_through_experts_interface():
     bank = model.global_experts
     assert bank.config._experts_implementation == "mi355x"
     assert all(isinstance(layer.mlp.gate, MI355XTopKRouter) for layer in model.layers)
+    if main_grad:
+        for p in (bank.gate_up_proj, bank.down_proj):
+            p.main_grad = torch.zeros_like(p)
 
     g = torch.Generator().manual_seed(3)
     B, T, H, K = 2, 64, cfg.hidden_size, cfg.num_experts_per_tok
@@ -289,9 +294,14 @@ def test_global_bank_dispatches_through_experts_interface():
         _, _, dw1, dw2, _ = O.experts_backward(cache, flat, w, w1c, w2c, d.reshape(-1, H))
         acc1 += dw1.double()
         acc2 += dw2.double()
-    e1 = (bank.gate_up_proj.grad.double().cpu() - acc1).abs().max() / acc1.abs().max()
-    e2 = (bank.down_proj.grad.double().cpu() - acc2).abs().max() / acc2.abs().max()
-    print(f"global bank dW over two calls: {e1:.2e} {e2:.2e}", flush=True)
+    if main_grad:
+        assert bank.gate_up_proj.grad is None and bank.down_proj.grad is None
+        g1, g2 = bank.gate_up_proj.main_grad, bank.down_proj.main_grad
+    else:
+        g1, g2 = bank.gate_up_proj.grad, bank.down_proj.grad
+    e1 = (g1.double().cpu() - acc1).abs().max() / acc1.abs().max()
+    e2 = (g2.double().cpu() - acc2).abs().max() / acc2.abs().max()
+    print(f"global bank dW over two calls (main_grad={main_grad}): {e1:.2e} {e2:.2e}", flush=True)
     assert e1 < 2e-2 and e2 < 2e-2
 
 
