@@ -256,7 +256,10 @@ def test_retrofit_dw_schedule_at_1792_experts():
     """The dW GEMMs' claimed-tile schedule at the Retrofit bank (E = 1792,
     Retrofit routing): the three dW GEMMs, writing into NaN-filled outputs,
     bit-identical to the static walk on two launches in a row (the 1437 or so
-    experts without rows included), and the schedule tables well-formed."""
+    experts without rows included), and the schedule tables well-formed;
+    then the two accumulating forms (fused gradient accumulation into the
+    bank's main_grad) at the full bank: acc += dW bit for bit as torch's bf16
+    add gives it, the experts without rows (NaN-filled) untouched."""
     from test_gpu_experts import _check_sched
     cfg = CONFIGS["retrofit"]
     inp = _inputs("retrofit")
@@ -287,6 +290,19 @@ def test_retrofit_dw_schedule_at_1792_experts():
         del d1, d2, d3
     load = _check_sched(plan, S, E)
     print(f"retrofit per-XCD rows {load}", flush=True)
+    empty = plan.counts == 0
+    for ref, fn, args in ((ref1, ops.gemm_gate_up_backward_dw_accumulate, (dgu, inp.x, plan)),
+                          (ref3, ops.gemm_down_backward_dw_gathered_accumulate,
+                           (dout, act, plan))):
+        acc = torch.randn(ref.shape, generator=g, device=DEV).to(torch.bfloat16)
+        acc[empty] = nan
+        exp = acc.clone()
+        exp[~empty] += ref[~empty]
+        fn(*args, acc)
+        torch.cuda.synchronize()
+        assert torch.equal(acc.view(torch.int16), exp.view(torch.int16)), fn.__name__
+        del acc, exp
+    print("retrofit accumulating dW GEMMs ok", flush=True)
 
 
 def test_xs_standard_fp32_layer():
