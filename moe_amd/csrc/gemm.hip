@@ -281,13 +281,31 @@ __global__ __launch_bounds__(kWaves<BR> * 64, 1) void grouped_gemm_kernel(GemmAr
   const int xcd = blockIdx.x & 7, nslot = gridDim.x >> 3;
   const bool dyn = DW && p.queue != nullptr;
   const int per_e = p.n_rt * p.n_ct;
+  // Lane x (of 8) holds XCD x's first expert slot and the number of its
+  // experts to claim (all, or the xnz[x] with rows), read once: a claim then
+  // makes one memory round trip, its atomic.
+  int xs_lane = 0, xn_lane = 0;
+  if (dyn) {
+    const int x = lane & 7;
+    xs_lane = p.xstart[x];
+    xn_lane = p.accumulate ? p.xnz[x] : p.xstart[x + 1] - xs_lane;
+  }
   auto claim = [&]() -> int {
     int* box = (int*)smem;  // free: the previous tile's epilogue ended with a barrier
+    // (read out of the lanes by the whole wave, outside the one-lane branch)
+    int e0s[8], ns[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int x = (xcd + k) & 7;
+      e0s[k] = __builtin_amdgcn_readlane(xs_lane, x);
+      ns[k] = __builtin_amdgcn_readlane(xn_lane, x) * per_e;
+    }
     if (tid == 0) {
       int v = -1;
+#pragma unroll
       for (int k = 0; k < 8; ++k) {
         const int x = (xcd + k) & 7;
-        const int e0 = p.xstart[x], n = (p.accumulate ? p.xnz[x] : p.xstart[x + 1] - e0) * per_e;
+        const int e0 = e0s[k], n = ns[k];
         if (n == 0) continue;
         const int j = __hip_atomic_fetch_add(p.queue + x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (j < n) {
