@@ -2441,6 +2441,8 @@ int down_dw_gathered(const void* d_out, const void* act_w, const int32_t* row_sr
                      int H, int I, int dtype, void* d_down_proj, bool accumulate, void* stream,
                      const char* who) {
   MOE_REQUIRE(!accumulate || tile_plan, MOE_ERR_ARG, "%s: needs the tile plan", who);
+  MOE_REQUIRE(!accumulate || dtype == MOE_DTYPE_BF16, MOE_ERR_UNSUPPORTED,
+              "%s: bf16 gradients only", who);
   int rc = check_common(S, E, H, I, dtype, who);
   if (rc) return rc;
   MOE_REQUIRE(top_k >= 1 && S == T * top_k, MOE_ERR_ARG, "%s: S != T*top_k", who);
@@ -2494,6 +2496,8 @@ int gate_up_dw(const void* d_gate_up, const void* hidden_states, const int32_t* 
                int E, int H, int I, int dtype, void* d_gate_up_proj, bool accumulate,
                void* stream, const char* who) {
   MOE_REQUIRE(!accumulate || tile_plan, MOE_ERR_ARG, "%s: needs the tile plan", who);
+  MOE_REQUIRE(!accumulate || dtype == MOE_DTYPE_BF16, MOE_ERR_UNSUPPORTED,
+              "%s: bf16 gradients only", who);
   if (dtype == MOE_DTYPE_F32 && !accumulate)
     return f32_gate_up_dw((const float*)d_gate_up, (const float*)hidden_states, row_src, top_k,
                           offsets, T, S, E, H, I, (float*)d_gate_up_proj, (hipStream_t)stream);
