@@ -329,17 +329,17 @@ RECORDED_TRAFFIC = {
         "gather_backward": 201893637,
     },
     "M standard": {
-        "gemm_gate_up_swiglu": 5298209282,
-        "gemm_down": 2585489976,
-        "gemm_down_backward_dx_fused": 4083282218,
-        "gemm_down_backward_dw_gathered": 2665683965,
-        "gemm_gate_up_backward_dx": 4752061988,
-        "gemm_gate_up_backward_dw": 4350178253,
-        "torch_gating_linear": 147061259,
-        "router_linear_backward_dx": 147699669,
-        "router_linear_backward_dw": 176370177,
-        "combine": 1210118315,
-        "gather_backward": 1343246294,
+        "gemm_gate_up_swiglu": 5058396448,
+        "gemm_down": 2587789420,
+        "gemm_down_backward_dx_fused": 3937119063,
+        "gemm_down_backward_dw_gathered": 2680022403,
+        "gemm_gate_up_backward_dx": 4894430789,
+        "gemm_gate_up_backward_dw": 4329990543,
+        "torch_gating_linear": 147097438,
+        "router_linear_backward_dx": 147560983,
+        "router_linear_backward_dw": 176374337,
+        "combine": 1210121163,
+        "gather_backward": 1343266837,
     },
 }
 
